@@ -1,0 +1,82 @@
+// device_common.hpp -- shared device helpers for the gfx950 fused-op kernels.
+//
+// Every kernel translation unit is compiled with -ffp-contract=off and without
+// fast-math, so each `a * b + c` below is two IEEE-rounded operations, exactly
+// as the reference's Rust CPU operators evaluate them.  Division and sqrt use
+// HIP's default correctly-rounded binary32 lowering (__fdiv_rn / __fsqrt_rn).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace atlas {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+__device__ __forceinline__ float pow2i(int k) {  // 2^k, k in [-126, 127]
+    return __uint_as_float(static_cast<uint32_t>(k + 127) << 23);
+}
+
+// binary32 exp: Cody & Waite reduction x = n*ln2 + r (ln2 split into the
+// 9-bit head 355/512 and its tail so n*head is exact) followed by the
+// degree-7 Taylor polynomial of e^r on |r| <= ln2/2, evaluated in Horner form.
+// Uses only IEEE add/sub/mul, floor and exponent-field assembly, so the
+// result is a deterministic function of x (faithfully rounded: < 1 ulp
+// against float64 exp over the finite range).
+__device__ __forceinline__ float exp_f32(float x) {
+    if (x != x) return x;
+    if (x > 89.0f) return __builtin_inff();
+    if (x < -104.0f) return 0.0f;
+    const float log2e = 1.44269502162933349609375f;
+    const float ln2_hi = 0.693359375f;
+    const float ln2_lo = -2.12194440e-4f;
+    float fn = floorf(x * log2e + 0.5f);
+    int n = static_cast<int>(fn);
+    float r = (x - fn * ln2_hi) - fn * ln2_lo;
+    float poly = 1.0f / 5040.0f;
+    poly = 1.0f / 720.0f + r * poly;
+    poly = 1.0f / 120.0f + r * poly;
+    poly = 1.0f / 24.0f + r * poly;
+    poly = 1.0f / 6.0f + r * poly;
+    poly = 0.5f + r * poly;
+    float p = 1.0f + (r + (r * r) * poly);
+    if (n > 127) return (p * pow2i(127)) * pow2i(n - 127);
+    if (n < -126) return (p * pow2i(n + 100)) * pow2i(-100);
+    return p * pow2i(n);
+}
+
+// tanh through its exponential identity with saturation at |x| >= 10
+// (Atlas atlas_tanh_f32, crates/atlas-metal/src/kernels.metal:742-750).
+__device__ __forceinline__ float tanh_f32(float v) {
+    if (v >= 10.0f) return 1.0f;
+    if (v <= -10.0f) return -1.0f;
+    float e = exp_f32(2.0f * v);
+    return __fdiv_rn(e - 1.0f, e + 1.0f);
+}
+
+// x / (1 + e^-x)   (kernels.metal:27-36)
+__device__ __forceinline__ float silu_f32(float x) { return __fdiv_rn(x, 1.0f + exp_f32(-x)); }
+
+// tanh-GELU with the overflow guard (kernels.metal:752-767):
+// a = c0*(x + ((c1*x)*x)*x); inf(a) -> (a > 0 ? x : 0); else (0.5*x)*(1 + tanh(a)).
+__device__ __forceinline__ float gelu_tanh_f32(float x) {
+    float argument = 0.7978845608f * (x + 0.044715f * x * x * x);
+    if (__builtin_isinf(argument)) return argument > 0.0f ? x : 0.0f;
+    return 0.5f * x * (1.0f + tanh_f32(argument));
+}
+
+// 1 / sqrt(mean + eps) with the CPU operators' two roundings
+// (phase_02_operators.rs:233-235: `.sqrt().recip()`).
+__device__ __forceinline__ float inverse_rms(float sum, float hidden, float epsilon) {
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(sum, hidden) + epsilon));
+}
+
+__device__ __forceinline__ float h2f(uint16_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, bits));
+}
+
+__device__ __forceinline__ uint16_t f2h(float v) {  // IEEE RNE
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+}  // namespace atlas

@@ -1,0 +1,213 @@
+// gather_kernels.hip -- token-embedding gathers (FP32, Q4_0, Q6_K) with the
+// sqrt(hidden) scale fused in, and the Gemma per-layer-embedding (PLE)
+// gather + dequant + combine.
+//
+// Reference semantics (bisegni/atlas):
+//   embedding_lookup_f32            crates/atlas-metal/src/kernels.metal:94-104
+//   embedding_lookup_q4_0           kernels.metal:653-656 (+ scalar_multiply_f32 :16-25)
+//   embedding_lookup_q6_k/q6_k_value kernels.metal:663-692
+//   block layouts / CPU dequant      crates/atlas-core/src/gguf.rs:379-438
+//   PLE chain                        crates/atlas-model/src/gemma4_executor.rs:4162-4237
+//                                    (gemma4_combine_ple crates/atlas-model/src/lib.rs:206-219)
+//
+// Layout on CDNA: one wavefront per gathered row (PLE: one 256-thread block
+// per token).  The packed row (Q4_0: 18-byte blocks, Q6_K: 210-byte blocks,
+// so rows are only 2/4/16-byte aligned depending on the width) is pulled into
+// LDS with the widest coalesced load its alignment allows, then every lane
+// unpacks four consecutive outputs from LDS with 16-bit reads and writes them
+// with one 128-bit store.  Every dequantised value is exact in f32
+// ((code - 8) * d for Q4_0; (code - 32) * scale * d for Q6_K), and the
+// scale/combine steps keep the reference's rounding order, so outputs are
+// bit-identical to the CPU dequant + scalar ops.
+#include "device_common.hpp"
+#include "launch.hpp"
+
+namespace atlas {
+namespace {
+
+__device__ __forceinline__ uint32_t lds_u16(const uint8_t* p) {  // p is 2-byte aligned
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+// Four consecutive Q4_0 values starting at column `col` (col % 4 == 0).
+__device__ __forceinline__ void q4_0_decode4(const uint8_t* row, uint32_t col, float v[4]) {
+    const uint32_t blk = (col >> 5) * 18;
+    const uint32_t k = col & 31;
+    const float d = h2f(static_cast<uint16_t>(lds_u16(row + blk)));
+    const uint32_t off = blk + 2 + (k & 15);  // even
+    const uint32_t lo = lds_u16(row + off), hi = lds_u16(row + off + 2);
+    const uint32_t bytes = lo | (hi << 16);
+    const uint32_t shift = k < 16 ? 0 : 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int nib = static_cast<int>((bytes >> (8 * j + shift)) & 15u);
+        v[j] = static_cast<float>(nib - 8) * d;
+    }
+}
+
+// Four consecutive Q6_K values starting at column `col` (col % 4 == 0).
+__device__ __forceinline__ void q6_k_decode4(const uint8_t* row, uint32_t col, float v[4]) {
+    const uint32_t blk = (col >> 8) * 210;
+    const uint32_t i = col & 255;
+    const uint32_t half = i >> 7, w = i & 127, st = w >> 5, l = w & 31;
+    const uint32_t ql_off = blk + half * 64 + l + ((st & 1) ? 32 : 0);
+    const uint32_t qh_off = blk + 128 + half * 32 + l;
+    const uint32_t ql = lds_u16(row + ql_off) | (lds_u16(row + ql_off + 2) << 16);
+    const uint32_t qh = lds_u16(row + qh_off) | (lds_u16(row + qh_off + 2) << 16);
+    const float sc = static_cast<float>(static_cast<int8_t>(row[blk + 192 + half * 8 + (l >> 4) + 2 * st]));
+    const float d = h2f(static_cast<uint16_t>(lds_u16(row + blk + 208)));
+    const uint32_t lshift = st >= 2 ? 4 : 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t low = (ql >> (8 * j + lshift)) & 15u;
+        const uint32_t high = (qh >> (8 * j + 2 * st)) & 3u;
+        const int q = static_cast<int>((high << 4) | low) - 32;
+        v[j] = static_cast<float>(q) * sc * d;
+    }
+}
+
+// Copy `bytes` (even) from global `src` to LDS `dst` with the widest
+// coalesced access the source alignment permits; threads [0, nthreads).
+__device__ __forceinline__ void stage_row(uint8_t* dst, const uint8_t* src, uint32_t bytes,
+                                          uint32_t tid, uint32_t nthreads) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(src);
+    if ((a & 15) == 0 && (bytes & 15) == 0) {
+        for (uint32_t i = tid; i < bytes / 16; i += nthreads)
+            reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+    } else if ((a & 3) == 0 && (bytes & 3) == 0) {
+        for (uint32_t i = tid; i < bytes / 4; i += nthreads)
+            reinterpret_cast<uint32_t*>(dst)[i] = reinterpret_cast<const uint32_t*>(src)[i];
+    } else {
+        for (uint32_t i = tid; i < bytes / 2; i += nthreads)
+            reinterpret_cast<uint16_t*>(dst)[i] = reinterpret_cast<const uint16_t*>(src)[i];
+    }
+}
+
+// FP32 gather: one wave per token, 4 tokens per block.
+__global__ __launch_bounds__(256) void embed_f32_kernel(const float* table, const uint32_t* ids, float* out,
+                                                        uint32_t vocab, uint32_t hidden, uint32_t tokens,
+                                                        float scale, int vec) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const uint32_t t = blockIdx.x * 4 + threadIdx.x / kWave;
+    if (t >= tokens) return;
+    const uint32_t id = ids[t];
+    float* dst = out + static_cast<size_t>(t) * hidden;
+    const bool valid = id < vocab;
+    const float* src = table + static_cast<size_t>(valid ? id : 0) * hidden;
+    const bool scaled = scale != 1.0f;
+    if (vec) {
+        for (uint32_t c = lane * 4; c < hidden; c += 4 * kWave) {
+            float4 v = valid ? *reinterpret_cast<const float4*>(src + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (scaled) v = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
+            *reinterpret_cast<float4*>(dst + c) = v;
+        }
+    } else {
+        for (uint32_t c = lane; c < hidden; c += kWave) {
+            float v = valid ? src[c] : 0.0f;
+            dst[c] = scaled ? v * scale : v;
+        }
+    }
+}
+
+// Q4_0 / Q6_K gather: one wave per token, 4 tokens per block, packed rows in LDS.
+template <bool Q6>
+__global__ __launch_bounds__(256) void embed_quant_kernel(const uint8_t* table, const uint32_t* ids, float* out,
+                                                          uint32_t vocab, uint32_t hidden, uint32_t tokens,
+                                                          float scale) {
+    extern __shared__ uint8_t lds[];
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t t = blockIdx.x * 4 + wave;
+    const uint32_t id = t < tokens ? ids[t] : vocab;
+    // the reference kernels leave rows with id >= vocab untouched
+    const bool active = id < vocab;
+    const uint32_t row_bytes = Q6 ? (hidden / 256) * 210 : (hidden / 32) * 18;
+    const uint32_t pitch = (row_bytes + 15) & ~15u;
+    uint8_t* row = lds + wave * pitch;
+    if (active) stage_row(row, table + static_cast<size_t>(id) * row_bytes, row_bytes, lane, kWave);
+    __syncthreads();  // every wave of the block reaches this barrier
+    if (!active) return;
+    float* dst = out + static_cast<size_t>(t) * hidden;
+    for (uint32_t c = lane * 4; c < hidden; c += 4 * kWave) {
+        float v[4];
+        if (Q6)
+            q6_k_decode4(row, c, v);
+        else
+            q4_0_decode4(row, c, v);
+        *reinterpret_cast<float4*>(dst + c) = make_float4(v[0] * scale, v[1] * scale, v[2] * scale, v[3] * scale);
+    }
+}
+
+// PLE: one 256-thread block per token.
+//   out[t, j] = ((deq(table[id])[j] * embedding_scale) + projection[t, j]) * output_scale
+template <bool Q6>
+__global__ __launch_bounds__(256) void ple_quant_kernel(const uint8_t* table, const uint32_t* ids,
+                                                        const float* projection, float* out, uint32_t vocab,
+                                                        uint32_t row_elems, uint32_t tokens,
+                                                        float embedding_scale, float output_scale) {
+    extern __shared__ uint8_t row[];
+    const uint32_t t = blockIdx.x;
+    if (t >= tokens) return;
+    const uint32_t id = ids[t];
+    if (id >= vocab) return;
+    const uint32_t row_bytes = Q6 ? (row_elems / 256) * 210 : (row_elems / 32) * 18;
+    stage_row(row, table + static_cast<size_t>(id) * row_bytes, row_bytes, threadIdx.x, blockDim.x);
+    __syncthreads();
+    const size_t base = static_cast<size_t>(t) * row_elems;
+    for (uint32_t c = threadIdx.x * 4; c < row_elems; c += 4 * blockDim.x) {
+        float v[4];
+        if (Q6)
+            q6_k_decode4(row, c, v);
+        else
+            q4_0_decode4(row, c, v);
+        const float4 p = *reinterpret_cast<const float4*>(projection + base + c);
+        float4 r;
+        r.x = (v[0] * embedding_scale + p.x) * output_scale;
+        r.y = (v[1] * embedding_scale + p.y) * output_scale;
+        r.z = (v[2] * embedding_scale + p.z) * output_scale;
+        r.w = (v[3] * embedding_scale + p.w) * output_scale;
+        *reinterpret_cast<float4*>(out + base + c) = r;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_embed_f32(hipStream_t stream, const float* table, const uint32_t* ids, float* out,
+                            uint32_t vocab, uint32_t hidden, uint32_t tokens, float scale) {
+    const int vec = (hidden % 4) == 0 && (reinterpret_cast<uintptr_t>(table) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+    hipLaunchKernelGGL(embed_f32_kernel, dim3((tokens + 3) / 4), dim3(256), 0, stream, table, ids, out, vocab,
+                       hidden, tokens, scale, vec);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_quant(hipStream_t stream, int q6k, const uint8_t* table, const uint32_t* ids,
+                              float* out, uint32_t vocab, uint32_t hidden, uint32_t tokens, float scale) {
+    const uint32_t row_bytes = q6k ? (hidden / 256) * 210 : (hidden / 32) * 18;
+    const size_t lds = 4 * static_cast<size_t>((row_bytes + 15) & ~15u);
+    const dim3 grid((tokens + 3) / 4);
+    if (q6k)
+        hipLaunchKernelGGL((embed_quant_kernel<true>), grid, dim3(256), lds, stream, table, ids, out, vocab,
+                           hidden, tokens, scale);
+    else
+        hipLaunchKernelGGL((embed_quant_kernel<false>), grid, dim3(256), lds, stream, table, ids, out, vocab,
+                           hidden, tokens, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_ple_quant(hipStream_t stream, int q6k, const uint8_t* table, const uint32_t* ids,
+                            const float* projection, float* out, uint32_t vocab, uint32_t layers,
+                            uint32_t width, uint32_t tokens, float embedding_scale, float output_scale) {
+    const uint32_t row_elems = layers * width;
+    const uint32_t row_bytes = q6k ? (row_elems / 256) * 210 : (row_elems / 32) * 18;
+    const size_t lds = (row_bytes + 15) & ~15u;
+    if (q6k)
+        hipLaunchKernelGGL((ple_quant_kernel<true>), dim3(tokens), dim3(256), lds, stream, table, ids, projection,
+                           out, vocab, row_elems, tokens, embedding_scale, output_scale);
+    else
+        hipLaunchKernelGGL((ple_quant_kernel<false>), dim3(tokens), dim3(256), lds, stream, table, ids, projection,
+                           out, vocab, row_elems, tokens, embedding_scale, output_scale);
+    return hipGetLastError();
+}
+
+}  // namespace atlas

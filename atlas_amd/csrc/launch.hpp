@@ -1,0 +1,94 @@
+// launch.hpp -- internal (C++) launch entry points between the C-ABI layer
+// (capi.hip) and the kernel translation units.  Each launcher assumes its
+// arguments were validated by the caller and enqueues work on `stream`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace atlas {
+
+// Reduction order of the row sums of squares.
+enum Reduction : int {
+    kSequential = 0,  // left-to-right f32 fold: bit-identical to the CPU operators
+    kWide = 1,        // lane-parallel partial sums + cross-lane tree (tolerance-level)
+};
+
+// RMSNorm family (norm_kernels.hip).  Modes of the row epilogue:
+enum NormMode : int {
+    kNormPlain = 0,     // y = (x*inv)*w
+    kNormResidual = 1,  // n = (x*inv)*w; [normalized = n]; out = residual + n
+    kNormAddNorm = 2,   // r = x + residual -> residual_out; y = (r*inv)*w
+    kNormAddScale = 3,  // n = (x*inv)*w; state = (state + n) * (*scale)
+};
+
+struct NormArgs {
+    const float* x;
+    const float* weight;
+    const float* residual;
+    float* normalized;
+    float* residual_out;
+    float* out;
+    const float* scale;
+    uint32_t rows;
+    uint32_t hidden;
+    float epsilon;
+};
+
+hipError_t launch_rms_norm_f32(hipStream_t stream, NormMode mode, Reduction red, const NormArgs& a);
+hipError_t launch_rms_norm_groups_stable_f32(hipStream_t stream, Reduction red, float* values,
+                                             const float* weight, uint32_t width, uint32_t groups,
+                                             float epsilon);
+hipError_t launch_rms_norm_f16(hipStream_t stream, Reduction red, const uint16_t* x,
+                               const uint16_t* residual, const uint16_t* weight,
+                               uint16_t* residual_out, uint16_t* out, uint32_t rows,
+                               uint32_t hidden, float epsilon);
+
+// RoPE (rope_kernels.hip).
+hipError_t launch_qk_norm_rope_f32(hipStream_t stream, Reduction red, const float* q,
+                                   const float* k, const float* q_weight, const float* k_weight,
+                                   const float* cosine, const float* sine, float* q_out,
+                                   float* k_out, uint32_t tokens, uint32_t q_heads,
+                                   uint32_t has_key, uint32_t head_dim, uint32_t rope_stride,
+                                   float epsilon);
+hipError_t launch_rope_half_f32(hipStream_t stream, const float* x, const float* cosine,
+                                const float* sine, float* out, uint32_t tokens, uint32_t heads,
+                                uint32_t head_dim, uint32_t rope_stride);
+hipError_t launch_rope_half_f16(hipStream_t stream, const uint16_t* x, const float* cosine,
+                                const float* sine, uint16_t* out, uint32_t tokens, uint32_t heads,
+                                uint32_t head_dim, uint32_t rope_stride);
+hipError_t launch_rope_interleaved_f32(hipStream_t stream, const float* x, const float* cosine,
+                                       const float* sine, float* out, uint32_t rows,
+                                       uint32_t hidden);
+
+// Gated activations and elementwise ops (glu_kernels.hip).
+enum EltOp : int {
+    kEltSilu = 0,
+    kEltGelu = 1,
+    kEltSwiglu = 2,
+    kEltGeglu = 3,
+    kEltAdd = 4,
+    kEltMul = 5,
+    kEltScale = 6,
+};
+hipError_t launch_elementwise_f32(hipStream_t stream, EltOp op, const float* a, const float* b,
+                                  float scalar, float* out, uint64_t n);
+hipError_t launch_swiglu_f16(hipStream_t stream, const uint16_t* gate, const uint16_t* up,
+                             uint16_t* out, uint64_t n);
+hipError_t launch_geglu_offset_f32(hipStream_t stream, const float* gate, const float* ple,
+                                   float* out, uint32_t ple_offset, uint32_t ple_row_stride,
+                                   uint32_t width, uint32_t rows);
+
+// Gathers (gather_kernels.hip).
+hipError_t launch_embed_f32(hipStream_t stream, const float* table, const uint32_t* ids,
+                            float* out, uint32_t vocab, uint32_t hidden, uint32_t tokens,
+                            float scale);
+hipError_t launch_embed_quant(hipStream_t stream, int q6k, const uint8_t* table,
+                              const uint32_t* ids, float* out, uint32_t vocab, uint32_t hidden,
+                              uint32_t tokens, float scale);
+hipError_t launch_ple_quant(hipStream_t stream, int q6k, const uint8_t* table, const uint32_t* ids,
+                            const float* projection, float* out, uint32_t vocab, uint32_t layers,
+                            uint32_t width, uint32_t tokens, float embedding_scale,
+                            float output_scale);
+
+}  // namespace atlas

@@ -1,0 +1,443 @@
+// norm_kernels.hip -- RMSNorm family for gfx950.
+//
+// Reference semantics (bisegni/atlas):
+//   rms_norm_f32                 crates/atlas-metal/src/kernels.metal:106-114
+//   gemma4_rms_residual_f32      kernels.metal:183-214
+//   gemma4_ple_rms_add_scale_f32 kernels.metal:228-258
+//   vector_add + rms_norm        crates/atlas-model/src/executor.rs:1258-1286
+//   rms_norm_groups_in_place_stable_f32  kernels.metal:897-917
+//   CPU operator (parity target) crates/atlas-ops/tests/phase_02_operators.rs:223-242
+//
+// Two reduction orders for the per-row sum of squares:
+//
+//  * Sequential (default).  The CPU operator folds x_i*x_i left to right in
+//    f32.  Fused epilogues (residual add, RoPE rotation) cancel, so any other
+//    order shows up as >1e-5 relative error on some elements; this engine
+//    reproduces the fold bit-for-bit.  One wavefront owns ROWS rows: all 64
+//    lanes stream the rows with 128-bit coalesced loads and write the squares
+//    to LDS (row stride hidden+4 floats, so the ROWS chain lanes hit distinct
+//    bank groups), then lane r folds row r's squares from LDS with
+//    ds_read_b128 in index order, and all lanes apply the epilogue.  Rows are
+//    fully read before any output is written, so in-place and aliased calls
+//    (x == out, normalized == x, residual_out == x) are safe.
+//
+//  * Wide.  One wavefront per row, per-lane partial sums and a cross-lane
+//    butterfly: the reference's rms_norm_decode_batch_f32 strategy
+//    (kernels.metal:119-133).  Tolerance-level against the CPU operator.
+#include "device_common.hpp"
+#include "launch.hpp"
+
+#include <stdlib.h>
+
+namespace atlas {
+namespace {
+
+struct f4 {
+    float x, y, z, w;
+};
+
+__device__ __forceinline__ f4 ld4(const float* p) {
+    float4 v = *reinterpret_cast<const float4*>(p);
+    return {v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ void st4(float* p, f4 v) {
+    *reinterpret_cast<float4*>(p) = make_float4(v.x, v.y, v.z, v.w);
+}
+
+// Row epilogue shared by both engines.  `inv` is the row's inverse RMS.
+template <int MODE>
+__device__ __forceinline__ float epilogue(const NormArgs& a, size_t idx, float xv, float inv,
+                                          float w, float scale) {
+    float n = xv * inv * w;
+    if (MODE == kNormPlain || MODE == kNormAddNorm) return n;
+    if (MODE == kNormResidual) {
+        if (a.normalized) a.normalized[idx] = n;
+        return a.residual[idx] + n;
+    }
+    // kNormAddScale: out aliases state
+    return (a.out[idx] + n) * scale;
+}
+
+template <int ROWS, int MODE, bool VEC>
+__global__ __launch_bounds__(64) void rms_seq_kernel(NormArgs a) {
+    extern __shared__ float lds[];
+    const uint32_t lane = threadIdx.x;
+    const uint32_t h = a.hidden;
+    const uint32_t stride = VEC ? h + 4 : h + 1;
+    const uint32_t row0 = blockIdx.x * ROWS;
+    const uint32_t nrows = min(static_cast<uint32_t>(ROWS), a.rows - row0);
+    float* inv_lds = lds + ROWS * stride;
+
+    // Phase A: coalesced loads, squares to LDS.
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        if (r >= static_cast<int>(nrows)) break;
+        const size_t base = static_cast<size_t>(row0 + r) * h;
+        float* sq = lds + r * stride;
+        if (VEC) {
+            for (uint32_t c = lane * 4; c < h; c += 4 * kWave) {
+                f4 x = ld4(a.x + base + c);
+                if (MODE == kNormAddNorm) {
+                    f4 res = ld4(a.residual + base + c);
+                    x = {x.x + res.x, x.y + res.y, x.z + res.z, x.w + res.w};
+                    st4(a.residual_out + base + c, x);
+                }
+                st4(sq + c, {x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w});
+            }
+        } else {
+            for (uint32_t c = lane; c < h; c += kWave) {
+                float x = a.x[base + c];
+                if (MODE == kNormAddNorm) {
+                    x = x + a.residual[base + c];
+                    a.residual_out[base + c] = x;
+                }
+                sq[c] = x * x;
+            }
+        }
+    }
+    __syncthreads();
+
+    // Phase B: lane r folds row r in index order.
+    if (lane < nrows) {
+        const float* sq = lds + lane * stride;
+        float s = 0.0f;
+        if (VEC) {
+#pragma unroll 8
+            for (uint32_t c = 0; c < h; c += 4) {
+                float4 v = *reinterpret_cast<const float4*>(sq + c);
+                s = s + v.x;
+                s = s + v.y;
+                s = s + v.z;
+                s = s + v.w;
+            }
+        } else {
+            for (uint32_t c = 0; c < h; ++c) s = s + sq[c];
+        }
+        inv_lds[lane] = inverse_rms(s, static_cast<float>(h), a.epsilon);
+    }
+    __syncthreads();
+
+    // Phase C: epilogue.
+    const float scale = MODE == kNormAddScale ? *a.scale : 1.0f;
+    const float* src = MODE == kNormAddNorm ? a.residual_out : a.x;
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        if (r >= static_cast<int>(nrows)) break;
+        const float inv = inv_lds[r];
+        const size_t base = static_cast<size_t>(row0 + r) * h;
+        if (VEC) {
+            for (uint32_t c = lane * 4; c < h; c += 4 * kWave) {
+                f4 x = ld4(src + base + c);
+                f4 w = ld4(a.weight + c);
+                f4 y;
+                y.x = epilogue<MODE>(a, base + c + 0, x.x, inv, w.x, scale);
+                y.y = epilogue<MODE>(a, base + c + 1, x.y, inv, w.y, scale);
+                y.z = epilogue<MODE>(a, base + c + 2, x.z, inv, w.z, scale);
+                y.w = epilogue<MODE>(a, base + c + 3, x.w, inv, w.w, scale);
+                st4(a.out + base + c, y);
+            }
+        } else {
+            for (uint32_t c = lane; c < h; c += kWave)
+                a.out[base + c] = epilogue<MODE>(a, base + c, src[base + c], inv, a.weight[c], scale);
+        }
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// Wide engine: one wave per row, 4 rows per 256-thread block.
+template <int MODE, bool VEC>
+__global__ __launch_bounds__(256) void rms_wide_kernel(NormArgs a) {
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const uint32_t row = blockIdx.x * 4 + threadIdx.x / kWave;
+    if (row >= a.rows) return;
+    const uint32_t h = a.hidden;
+    const size_t base = static_cast<size_t>(row) * h;
+    float partial = 0.0f;
+    if (VEC) {
+        for (uint32_t c = lane * 4; c < h; c += 4 * kWave) {
+            f4 x = ld4(a.x + base + c);
+            if (MODE == kNormAddNorm) {
+                f4 res = ld4(a.residual + base + c);
+                x = {x.x + res.x, x.y + res.y, x.z + res.z, x.w + res.w};
+                st4(a.residual_out + base + c, x);
+            }
+            partial = partial + x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+        }
+    } else {
+        for (uint32_t c = lane; c < h; c += kWave) {
+            float x = a.x[base + c];
+            if (MODE == kNormAddNorm) {
+                x = x + a.residual[base + c];
+                a.residual_out[base + c] = x;
+            }
+            partial = partial + x * x;
+        }
+    }
+    const float inv = inverse_rms(wave_sum(partial), static_cast<float>(h), a.epsilon);
+    const float scale = MODE == kNormAddScale ? *a.scale : 1.0f;
+    const float* src = MODE == kNormAddNorm ? a.residual_out : a.x;
+    if (VEC) {
+        for (uint32_t c = lane * 4; c < h; c += 4 * kWave) {
+            f4 x = ld4(src + base + c);
+            f4 w = ld4(a.weight + c);
+            f4 y;
+            y.x = epilogue<MODE>(a, base + c + 0, x.x, inv, w.x, scale);
+            y.y = epilogue<MODE>(a, base + c + 1, x.y, inv, w.y, scale);
+            y.z = epilogue<MODE>(a, base + c + 2, x.z, inv, w.z, scale);
+            y.w = epilogue<MODE>(a, base + c + 3, x.w, inv, w.w, scale);
+            st4(a.out + base + c, y);
+        }
+    } else {
+        for (uint32_t c = lane; c < h; c += kWave)
+            a.out[base + c] = epilogue<MODE>(a, base + c, src[base + c], inv, a.weight[c], scale);
+    }
+}
+
+int env_int(const char* name, int fallback) {
+    const char* v = getenv(name);
+    if (!v || !*v) return fallback;
+    return atoi(v);
+}
+
+// Rows per wavefront for the sequential engine: enough wavefronts to keep
+// every SIMD streaming (>= 2048 for large row counts), bounded by 64 KB LDS.
+int pick_rows(uint32_t rows, uint32_t hidden) {
+    static const int forced = env_int("ATLAS_SEQ_ROWS", 0);
+    int best = 1;
+    for (int r : {2, 4, 8, 16}) {
+        size_t lds = (static_cast<size_t>(r) * (hidden + 4) + r) * 4;
+        if (lds > 65536) break;
+        if ((rows + r - 1) / r >= 2048) best = r;
+    }
+    if (forced > 0) best = forced;
+    return best;
+}
+
+template <int ROWS, int MODE>
+hipError_t launch_seq_rows(hipStream_t s, const NormArgs& a, bool vec) {
+    const uint32_t stride = vec ? a.hidden + 4 : a.hidden + 1;
+    const size_t lds = (static_cast<size_t>(ROWS) * stride + ROWS) * sizeof(float);
+    const dim3 grid((a.rows + ROWS - 1) / ROWS);
+    if (vec)
+        hipLaunchKernelGGL((rms_seq_kernel<ROWS, MODE, true>), grid, dim3(kWave), lds, s, a);
+    else
+        hipLaunchKernelGGL((rms_seq_kernel<ROWS, MODE, false>), grid, dim3(kWave), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int MODE>
+hipError_t launch_seq(hipStream_t s, const NormArgs& a, bool vec) {
+    switch (pick_rows(a.rows, a.hidden)) {
+        case 16: return launch_seq_rows<16, MODE>(s, a, vec);
+        case 8: return launch_seq_rows<8, MODE>(s, a, vec);
+        case 4: return launch_seq_rows<4, MODE>(s, a, vec);
+        case 2: return launch_seq_rows<2, MODE>(s, a, vec);
+        default: return launch_seq_rows<1, MODE>(s, a, vec);
+    }
+}
+
+template <int MODE>
+hipError_t launch_wide(hipStream_t s, const NormArgs& a, bool vec) {
+    const dim3 grid((a.rows + 3) / 4);
+    if (vec)
+        hipLaunchKernelGGL((rms_wide_kernel<MODE, true>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((rms_wide_kernel<MODE, false>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// ---------------------------------------------------------------------------
+// Stable per-group RMSNorm (max-scaled), in place.  One wave per group:
+// m = max|v| is order-free (wave max), the (v/m)^2 fold is sequential in
+// index order on lane 0 from LDS, then all lanes rewrite the group.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void groups_stable_kernel(float* values, const float* weight,
+                                                           uint32_t width, uint32_t groups,
+                                                           float epsilon, int sequential) {
+    extern __shared__ float sq[];
+    const uint32_t g = blockIdx.x;
+    const uint32_t lane = threadIdx.x;
+    if (g >= groups) return;
+    float* v = values + static_cast<size_t>(g) * width;
+    float m = 0.0f;
+    for (uint32_t i = lane; i < width; i += kWave) m = fmaxf(m, fabsf(v[i]));
+    m = wave_max(m);
+    if (m == 0.0f) {
+        for (uint32_t i = lane; i < width; i += kWave) v[i] = 0.0f;
+        return;
+    }
+    float partial = 0.0f;
+    for (uint32_t i = lane; i < width; i += kWave) {
+        float scaled = __fdiv_rn(v[i], m);
+        float s2 = scaled * scaled;
+        if (sequential)
+            sq[i] = s2;
+        else
+            partial = partial + s2;
+    }
+    float sum;
+    if (sequential) {
+        __syncthreads();
+        __shared__ float total;
+        if (lane == 0) {
+            float s = 0.0f;
+            for (uint32_t i = 0; i < width; ++i) s = s + sq[i];
+            total = s;
+        }
+        __syncthreads();
+        sum = total;
+    } else {
+        sum = wave_sum(partial);
+    }
+    const float root = __fsqrt_rn(__fdiv_rn(sum, static_cast<float>(width)) + __fdiv_rn(epsilon, m * m));
+    const float inv = __fdiv_rn(__fdiv_rn(1.0f, root), m);
+    for (uint32_t i = lane; i < width; i += kWave) v[i] = v[i] * inv * weight[i];
+}
+
+// ---------------------------------------------------------------------------
+// FP16-storage RMSNorm (optionally fused with the pre-norm residual add).
+// Storage f16, math f32: widening is exact, outputs are rounded RNE.  With a
+// residual, r = rne16(x + residual) is stored and the norm reads the stored
+// value, matching the two-kernel chain with f16 buffers.
+// ---------------------------------------------------------------------------
+struct h8 {
+    uint16_t v[8];
+};
+
+template <bool ADD>
+__global__ __launch_bounds__(64) void rms_f16_seq_kernel(const uint16_t* x, const uint16_t* residual,
+                                                         const uint16_t* weight,
+                                                         uint16_t* residual_out, uint16_t* out,
+                                                         uint32_t rows, uint32_t hidden,
+                                                         float epsilon, int sequential) {
+    extern __shared__ float sq[];
+    __shared__ float inv_shared;
+    const uint32_t row = blockIdx.x;
+    const uint32_t lane = threadIdx.x;
+    if (row >= rows) return;
+    const size_t base = static_cast<size_t>(row) * hidden;
+    const bool vec = (hidden % 8) == 0;
+    float partial = 0.0f;
+    if (vec) {
+        for (uint32_t c = lane * 8; c < hidden; c += 8 * kWave) {
+            h8 a = *reinterpret_cast<const h8*>(x + base + c);
+            if (ADD) {
+                h8 b = *reinterpret_cast<const h8*>(residual + base + c);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) a.v[j] = f2h(h2f(a.v[j]) + h2f(b.v[j]));
+                *reinterpret_cast<h8*>(residual_out + base + c) = a;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float f = h2f(a.v[j]);
+                if (sequential)
+                    sq[c + j] = f * f;
+                else
+                    partial = partial + f * f;
+            }
+        }
+    } else {
+        for (uint32_t c = lane; c < hidden; c += kWave) {
+            uint16_t a = x[base + c];
+            if (ADD) {
+                a = f2h(h2f(a) + h2f(residual[base + c]));
+                residual_out[base + c] = a;
+            }
+            float f = h2f(a);
+            if (sequential)
+                sq[c] = f * f;
+            else
+                partial = partial + f * f;
+        }
+    }
+    float inv;
+    if (sequential) {
+        __syncthreads();
+        if (lane == 0) {
+            float s = 0.0f;
+            for (uint32_t c = 0; c < hidden; ++c) s = s + sq[c];
+            inv_shared = inverse_rms(s, static_cast<float>(hidden), epsilon);
+        }
+        __syncthreads();
+        inv = inv_shared;
+    } else {
+        inv = inverse_rms(wave_sum(partial), static_cast<float>(hidden), epsilon);
+    }
+    const uint16_t* src = ADD ? residual_out : x;
+    if (vec) {
+        for (uint32_t c = lane * 8; c < hidden; c += 8 * kWave) {
+            h8 a = *reinterpret_cast<const h8*>(src + base + c);
+            h8 w = *reinterpret_cast<const h8*>(weight + c);
+            h8 y;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) y.v[j] = f2h(h2f(a.v[j]) * inv * h2f(w.v[j]));
+            *reinterpret_cast<h8*>(out + base + c) = y;
+        }
+    } else {
+        for (uint32_t c = lane; c < hidden; c += kWave)
+            out[base + c] = f2h(h2f(src[base + c]) * inv * h2f(weight[c]));
+    }
+}
+
+}  // namespace
+
+hipError_t launch_rms_norm_f32(hipStream_t stream, NormMode mode, Reduction red, const NormArgs& a) {
+    bool vec = (a.hidden % 4) == 0 && aligned16(a.x) && aligned16(a.weight) && aligned16(a.out) &&
+               (!a.residual || aligned16(a.residual)) && (!a.normalized || aligned16(a.normalized)) &&
+               (!a.residual_out || aligned16(a.residual_out));
+    if (red == kWide) {
+        switch (mode) {
+            case kNormPlain: return launch_wide<kNormPlain>(stream, a, vec);
+            case kNormResidual: return launch_wide<kNormResidual>(stream, a, vec);
+            case kNormAddNorm: return launch_wide<kNormAddNorm>(stream, a, vec);
+            case kNormAddScale: return launch_wide<kNormAddScale>(stream, a, vec);
+        }
+    } else {
+        switch (mode) {
+            case kNormPlain: return launch_seq<kNormPlain>(stream, a, vec);
+            case kNormResidual: return launch_seq<kNormResidual>(stream, a, vec);
+            case kNormAddNorm: return launch_seq<kNormAddNorm>(stream, a, vec);
+            case kNormAddScale: return launch_seq<kNormAddScale>(stream, a, vec);
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_rms_norm_groups_stable_f32(hipStream_t stream, Reduction red, float* values,
+                                             const float* weight, uint32_t width, uint32_t groups,
+                                             float epsilon) {
+    const size_t lds = red == kSequential ? static_cast<size_t>(width) * sizeof(float) : 0;
+    hipLaunchKernelGGL(groups_stable_kernel, dim3(groups), dim3(kWave), lds, stream, values, weight,
+                       width, groups, epsilon, red == kSequential ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm_f16(hipStream_t stream, Reduction red, const uint16_t* x,
+                               const uint16_t* residual, const uint16_t* weight,
+                               uint16_t* residual_out, uint16_t* out, uint32_t rows,
+                               uint32_t hidden, float epsilon) {
+    const int seq = red == kSequential ? 1 : 0;
+    const size_t lds = seq ? static_cast<size_t>(hidden) * sizeof(float) : 0;
+    if (residual)
+        hipLaunchKernelGGL((rms_f16_seq_kernel<true>), dim3(rows), dim3(kWave), lds, stream, x,
+                           residual, weight, residual_out, out, rows, hidden, epsilon, seq);
+    else
+        hipLaunchKernelGGL((rms_f16_seq_kernel<false>), dim3(rows), dim3(kWave), lds, stream, x,
+                           residual, weight, residual_out, out, rows, hidden, epsilon, seq);
+    return hipGetLastError();
+}
+
+}  // namespace atlas

@@ -1,0 +1,449 @@
+// rope_kernels.hip -- per-head QK-RMSNorm fused with half-split RoPE, plain
+// half-split RoPE (f32 / f16 storage) and the interleaved operator-API RoPE.
+//
+// Reference semantics (bisegni/atlas):
+//   gemma4_qk_norm_rope_fused_batch_f32   crates/atlas-metal/src/kernels.metal:1098-1142
+//   (exact oracle kernel; the _wide variants at :1053-1090, :1151-1195 reorder
+//   the sum of squares)
+//   Llama half-split RoPE = rope_half_to_interleaved_f32 + rope_f32 +
+//   rope_interleaved_to_half_f32   kernels.metal:940-949, 972-994
+//   NeuralOps::rope (interleaved) = rope_f32; CPU oracle cpu_rope
+//   crates/atlas-ops/tests/phase_02_operators.rs:262-272
+//
+// QK-norm+RoPE mapping on CDNA: a "unit" is one (token, head) row of
+// head_dim floats; Q heads come first, then the optional single K head.  One
+// wavefront owns UNITS consecutive units.  With head_dim = 64*V every lane
+// holds V consecutive floats of each unit in registers (one 128-bit load for
+// V = 4), and the RoPE partner x[p + d/2] of the value x[p] held by lane l
+// sits in lane l^32, so the pair is exchanged with one cross-lane swap and
+// never round-trips through memory.  The squares go to LDS for the
+// sequential fold (lane u folds unit u in index order), which makes the
+// result bit-identical to the CPU composition rms_norm -> rope.
+#include "device_common.hpp"
+#include "launch.hpp"
+
+namespace atlas {
+namespace {
+
+template <int V>
+struct vecf {
+    float v[V];
+};
+
+template <int V>
+__device__ __forceinline__ vecf<V> ldv(const float* p) {
+    vecf<V> r;
+    if constexpr (V == 2) {
+        float2 a = *reinterpret_cast<const float2*>(p);
+        r.v[0] = a.x;
+        r.v[1] = a.y;
+    } else if constexpr (V == 4) {
+        float4 a = *reinterpret_cast<const float4*>(p);
+        r.v[0] = a.x;
+        r.v[1] = a.y;
+        r.v[2] = a.z;
+        r.v[3] = a.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < V; j += 4) {
+            float4 a = *reinterpret_cast<const float4*>(p + j);
+            r.v[j] = a.x;
+            r.v[j + 1] = a.y;
+            r.v[j + 2] = a.z;
+            r.v[j + 3] = a.w;
+        }
+    }
+    return r;
+}
+
+template <int V>
+__device__ __forceinline__ void stv(float* p, const vecf<V>& r) {
+    if constexpr (V == 2) {
+        *reinterpret_cast<float2*>(p) = make_float2(r.v[0], r.v[1]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < V; j += 4)
+            *reinterpret_cast<float4*>(p + j) = make_float4(r.v[j], r.v[j + 1], r.v[j + 2], r.v[j + 3]);
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+template <int V, int UNITS, bool SEQ>
+__global__ __launch_bounds__(64) void qk_norm_rope_kernel(
+    const float* q, const float* k, const float* q_weight, const float* k_weight,
+    const float* cosine, const float* sine, float* q_out, float* k_out, uint32_t tokens,
+    uint32_t q_heads, uint32_t has_key, uint32_t rope_stride, float epsilon) {
+    constexpr uint32_t D = 64 * V;
+    constexpr uint32_t HALF = D / 2;
+    constexpr uint32_t STRIDE = D + 4;
+    __shared__ float sq[SEQ ? UNITS * STRIDE : 1];
+    __shared__ float inv_lds[UNITS];
+
+    const uint32_t lane = threadIdx.x;
+    const uint32_t total = q_heads + has_key;
+    const uint32_t units = tokens * total;
+    const uint32_t u0 = blockIdx.x * UNITS;
+    const bool low = lane < 32;
+    const uint32_t col = lane * V;                        // this lane's first column
+    const uint32_t pair = low ? col : col - HALF;         // first RoPE pair index
+    const uint32_t partner_col = low ? col + HALF : col - HALF;
+
+    vecf<V> x[UNITS];
+#pragma unroll
+    for (int u = 0; u < UNITS; ++u) {
+        const uint32_t unit = u0 + u;
+        if (unit < units) {
+            const uint32_t t = unit / total, local = unit % total;
+            const float* src = local >= q_heads ? k + static_cast<size_t>(t) * D
+                                                : q + (static_cast<size_t>(t) * q_heads + local) * D;
+            x[u] = ldv<V>(src + col);
+        } else {
+#pragma unroll
+            for (int j = 0; j < V; ++j) x[u].v[j] = 0.0f;
+        }
+    }
+
+    if constexpr (SEQ) {
+#pragma unroll
+        for (int u = 0; u < UNITS; ++u) {
+            vecf<V> s2;
+#pragma unroll
+            for (int j = 0; j < V; ++j) s2.v[j] = x[u].v[j] * x[u].v[j];
+            stv<V>(sq + u * STRIDE + col, s2);
+        }
+        __syncthreads();
+        if (lane < UNITS) {
+            const float* row = sq + lane * STRIDE;
+            float s = 0.0f;
+#pragma unroll 8
+            for (uint32_t c = 0; c < D; c += 4) {
+                float4 v = *reinterpret_cast<const float4*>(row + c);
+                s = s + v.x;
+                s = s + v.y;
+                s = s + v.z;
+                s = s + v.w;
+            }
+            inv_lds[lane] = inverse_rms(s, static_cast<float>(D), epsilon);
+        }
+        __syncthreads();
+    } else {
+#pragma unroll
+        for (int u = 0; u < UNITS; ++u) {
+            float partial = 0.0f;
+#pragma unroll
+            for (int j = 0; j < V; ++j) partial = partial + x[u].v[j] * x[u].v[j];
+            float s = wave_sum(partial);
+            if (lane == 0) inv_lds[u] = inverse_rms(s, static_cast<float>(D), epsilon);
+        }
+        __syncthreads();
+    }
+
+    const vecf<V> qw_own = ldv<V>(q_weight + col), qw_par = ldv<V>(q_weight + partner_col);
+    vecf<V> kw_own = qw_own, kw_par = qw_par;
+    if (has_key) {
+        kw_own = ldv<V>(k_weight + col);
+        kw_par = ldv<V>(k_weight + partner_col);
+    }
+
+#pragma unroll
+    for (int u = 0; u < UNITS; ++u) {
+        const uint32_t unit = u0 + u;
+        // exchange halves: lane l <-> lane l^32 (executed by the whole wave)
+        vecf<V> other;
+#pragma unroll
+        for (int j = 0; j < V; ++j) other.v[j] = __shfl_xor(x[u].v[j], 32, kWave);
+        if (unit >= units) continue;
+        const uint32_t t = unit / total, local = unit % total;
+        const bool key = local >= q_heads;
+        const float inv = inv_lds[u];
+        const vecf<V>& w_own = key ? kw_own : qw_own;
+        const vecf<V>& w_par = key ? kw_par : qw_par;
+        const vecf<V> c = ldv<V>(cosine + static_cast<size_t>(t) * rope_stride + pair);
+        const vecf<V> s = ldv<V>(sine + static_cast<size_t>(t) * rope_stride + pair);
+        vecf<V> y;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const float own = x[u].v[j] * inv * w_own.v[j];
+            const float par = other.v[j] * inv * w_par.v[j];
+            // low lanes hold x0 (own) and receive x1; high lanes the reverse
+            const float x0 = low ? own : par;
+            const float x1 = low ? par : own;
+            y.v[j] = low ? x0 * c.v[j] - x1 * s.v[j] : x0 * s.v[j] + x1 * c.v[j];
+        }
+        float* dst = key ? k_out + static_cast<size_t>(t) * D
+                         : q_out + (static_cast<size_t>(t) * q_heads + local) * D;
+        stv<V>(dst + col, y);
+    }
+}
+
+// Generic head_dim fallback (even head_dim not of the form 64*V): one wave
+// per unit, row staged in LDS.
+__global__ __launch_bounds__(64) void qk_norm_rope_generic_kernel(
+    const float* q, const float* k, const float* q_weight, const float* k_weight,
+    const float* cosine, const float* sine, float* q_out, float* k_out, uint32_t tokens,
+    uint32_t q_heads, uint32_t has_key, uint32_t head_dim, uint32_t rope_stride, float epsilon,
+    int sequential) {
+    extern __shared__ float row[];
+    __shared__ float inv_shared;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t total = q_heads + has_key;
+    const uint32_t unit = blockIdx.x;
+    if (unit >= tokens * total) return;
+    const uint32_t t = unit / total, local = unit % total;
+    const bool key = local >= q_heads;
+    const float* src = key ? k + static_cast<size_t>(t) * head_dim
+                           : q + (static_cast<size_t>(t) * q_heads + local) * head_dim;
+    float* dst = key ? k_out + static_cast<size_t>(t) * head_dim
+                     : q_out + (static_cast<size_t>(t) * q_heads + local) * head_dim;
+    const float* w = key ? k_weight : q_weight;
+    float partial = 0.0f;
+    for (uint32_t i = lane; i < head_dim; i += kWave) {
+        float v = src[i];
+        row[i] = v;
+        partial = partial + v * v;
+    }
+    __syncthreads();
+    float inv;
+    if (sequential) {
+        if (lane == 0) {
+            float s = 0.0f;
+            for (uint32_t i = 0; i < head_dim; ++i) s = s + row[i] * row[i];
+            inv_shared = inverse_rms(s, static_cast<float>(head_dim), epsilon);
+        }
+        __syncthreads();
+        inv = inv_shared;
+    } else {
+        inv = inverse_rms(wave_sum(partial), static_cast<float>(head_dim), epsilon);
+    }
+    const uint32_t half = head_dim / 2;
+    for (uint32_t p = lane; p < half; p += kWave) {
+        const float x0 = row[p] * inv * w[p];
+        const float x1 = row[p + half] * inv * w[p + half];
+        const float c = cosine[static_cast<size_t>(t) * rope_stride + p];
+        const float s = sine[static_cast<size_t>(t) * rope_stride + p];
+        dst[p] = x0 * c - x1 * s;
+        dst[p + half] = x0 * s + x1 * c;
+    }
+}
+
+// Half-split RoPE, 4 pairs per thread when half % 4 == 0, else 1.
+template <int P>
+__global__ __launch_bounds__(256) void rope_half_f32_kernel(const float* x, const float* cosine,
+                                                            const float* sine, float* out,
+                                                            uint32_t tokens, uint32_t heads,
+                                                            uint32_t head_dim, uint32_t rope_stride) {
+    const uint32_t half = head_dim / 2;
+    const uint32_t groups_per_unit = half / P;
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t total = static_cast<uint64_t>(tokens) * heads * groups_per_unit;
+    if (i >= total) return;
+    const uint64_t unit = i / groups_per_unit;
+    const uint32_t p = static_cast<uint32_t>(i % groups_per_unit) * P;
+    const uint32_t t = static_cast<uint32_t>(unit / heads);
+    const size_t base = unit * head_dim;
+    const size_t tb = static_cast<size_t>(t) * rope_stride + p;
+    float a[P], b[P], c[P], s[P];
+    if constexpr (P == 4) {
+        float4 va = *reinterpret_cast<const float4*>(x + base + p);
+        float4 vb = *reinterpret_cast<const float4*>(x + base + p + half);
+        a[0] = va.x; a[1] = va.y; a[2] = va.z; a[3] = va.w;
+        b[0] = vb.x; b[1] = vb.y; b[2] = vb.z; b[3] = vb.w;
+    } else {
+        a[0] = x[base + p];
+        b[0] = x[base + p + half];
+    }
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        c[j] = cosine[tb + j];
+        s[j] = sine[tb + j];
+    }
+    float o0[P], o1[P];
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        o0[j] = a[j] * c[j] - b[j] * s[j];
+        o1[j] = a[j] * s[j] + b[j] * c[j];
+    }
+    if constexpr (P == 4) {
+        *reinterpret_cast<float4*>(out + base + p) = make_float4(o0[0], o0[1], o0[2], o0[3]);
+        *reinterpret_cast<float4*>(out + base + p + half) = make_float4(o1[0], o1[1], o1[2], o1[3]);
+    } else {
+        out[base + p] = o0[0];
+        out[base + p + half] = o1[0];
+    }
+}
+
+struct h4 {
+    uint16_t v[4];
+};
+
+template <int P>
+__global__ __launch_bounds__(256) void rope_half_f16_kernel(const uint16_t* x, const float* cosine,
+                                                            const float* sine, uint16_t* out,
+                                                            uint32_t tokens, uint32_t heads,
+                                                            uint32_t head_dim, uint32_t rope_stride) {
+    const uint32_t half = head_dim / 2;
+    const uint32_t groups_per_unit = half / P;
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t total = static_cast<uint64_t>(tokens) * heads * groups_per_unit;
+    if (i >= total) return;
+    const uint64_t unit = i / groups_per_unit;
+    const uint32_t p = static_cast<uint32_t>(i % groups_per_unit) * P;
+    const uint32_t t = static_cast<uint32_t>(unit / heads);
+    const size_t base = unit * head_dim;
+    const size_t tb = static_cast<size_t>(t) * rope_stride + p;
+    uint16_t a[P], b[P];
+    if constexpr (P == 4) {
+        h4 va = *reinterpret_cast<const h4*>(x + base + p);
+        h4 vb = *reinterpret_cast<const h4*>(x + base + p + half);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            a[j] = va.v[j];
+            b[j] = vb.v[j];
+        }
+    } else {
+        a[0] = x[base + p];
+        b[0] = x[base + p + half];
+    }
+    uint16_t o0[P], o1[P];
+#pragma unroll
+    for (int j = 0; j < P; ++j) {
+        const float x0 = h2f(a[j]), x1 = h2f(b[j]);
+        const float c = cosine[tb + j], s = sine[tb + j];
+        o0[j] = f2h(x0 * c - x1 * s);
+        o1[j] = f2h(x0 * s + x1 * c);
+    }
+    if constexpr (P == 4) {
+        h4 r0, r1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            r0.v[j] = o0[j];
+            r1.v[j] = o1[j];
+        }
+        *reinterpret_cast<h4*>(out + base + p) = r0;
+        *reinterpret_cast<h4*>(out + base + p + half) = r1;
+    } else {
+        out[base + p] = o0[0];
+        out[base + p + half] = o1[0];
+    }
+}
+
+// Interleaved pairs (NeuralOps::rope): out[2p] = x0*c - x1*s, out[2p+1] = x0*s + x1*c,
+// one cos/sin row shared by every input row.
+__global__ __launch_bounds__(256) void rope_interleaved_kernel(const float* x, const float* cosine,
+                                                               const float* sine, float* out,
+                                                               uint32_t rows, uint32_t hidden) {
+    const uint32_t pairs = hidden / 2;
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<uint64_t>(rows) * pairs) return;
+    const uint32_t p = static_cast<uint32_t>(i % pairs);
+    const size_t b = (i / pairs) * hidden + 2 * p;
+    const float x0 = x[b], x1 = x[b + 1];
+    const float c = cosine[p], s = sine[p];
+    const float o0 = x0 * c - x1 * s;
+    const float o1 = x0 * s + x1 * c;
+    out[b] = o0;
+    out[b + 1] = o1;
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+template <int V, int UNITS>
+hipError_t launch_qk(hipStream_t s, bool seq, const float* q, const float* k, const float* qw,
+                     const float* kw, const float* c, const float* sn, float* qo, float* ko,
+                     uint32_t tokens, uint32_t q_heads, uint32_t has_key, uint32_t rope_stride,
+                     float eps) {
+    const uint32_t units = tokens * (q_heads + has_key);
+    const dim3 grid((units + UNITS - 1) / UNITS);
+    if (seq)
+        hipLaunchKernelGGL((qk_norm_rope_kernel<V, UNITS, true>), grid, dim3(kWave), 0, s, q, k, qw,
+                           kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
+    else
+        hipLaunchKernelGGL((qk_norm_rope_kernel<V, UNITS, false>), grid, dim3(kWave), 0, s, q, k, qw,
+                           kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_qk_norm_rope_f32(hipStream_t stream, Reduction red, const float* q, const float* k,
+                                   const float* q_weight, const float* k_weight,
+                                   const float* cosine, const float* sine, float* q_out,
+                                   float* k_out, uint32_t tokens, uint32_t q_heads,
+                                   uint32_t has_key, uint32_t head_dim, uint32_t rope_stride,
+                                   float epsilon) {
+    const bool seq = red == kSequential;
+    // Fast path: head_dim = 64*V, 16-byte aligned operands (8-byte for V=2),
+    // and per-token cos/sin rows aligned to the vector width.
+    const uintptr_t va = head_dim == 128 ? 8 : 16;
+    const bool vec_ok = (head_dim == 128 || head_dim == 256 || head_dim == 512) && aligned(q, va) &&
+                        aligned(q_out, va) && aligned(q_weight, va) && aligned(cosine, va) &&
+                        aligned(sine, va) && (rope_stride % (head_dim / 64)) == 0 &&
+                        (!has_key || (aligned(k, va) && aligned(k_out, va) && aligned(k_weight, va)));
+    if (vec_ok) {
+        if (head_dim == 256)
+            return launch_qk<4, 16>(stream, seq, q, k, q_weight, k_weight, cosine, sine, q_out, k_out,
+                                    tokens, q_heads, has_key, rope_stride, epsilon);
+        if (head_dim == 512)
+            return launch_qk<8, 8>(stream, seq, q, k, q_weight, k_weight, cosine, sine, q_out, k_out,
+                                   tokens, q_heads, has_key, rope_stride, epsilon);
+        return launch_qk<2, 16>(stream, seq, q, k, q_weight, k_weight, cosine, sine, q_out, k_out,
+                                tokens, q_heads, has_key, rope_stride, epsilon);
+    }
+    const uint32_t units = tokens * (q_heads + has_key);
+    hipLaunchKernelGGL(qk_norm_rope_generic_kernel, dim3(units), dim3(kWave),
+                       static_cast<size_t>(head_dim) * sizeof(float), stream, q, k, q_weight,
+                       k_weight, cosine, sine, q_out, k_out, tokens, q_heads, has_key, head_dim,
+                       rope_stride, epsilon, seq ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_half_f32(hipStream_t stream, const float* x, const float* cosine,
+                                const float* sine, float* out, uint32_t tokens, uint32_t heads,
+                                uint32_t head_dim, uint32_t rope_stride) {
+    const uint32_t half = head_dim / 2;
+    const bool vec = (half % 4) == 0 && aligned(x, 16) && aligned(out, 16);
+    const uint32_t P = vec ? 4 : 1;
+    const uint64_t threads = static_cast<uint64_t>(tokens) * heads * (half / P);
+    const dim3 grid(static_cast<uint32_t>((threads + 255) / 256));
+    if (vec)
+        hipLaunchKernelGGL((rope_half_f32_kernel<4>), grid, dim3(256), 0, stream, x, cosine, sine, out,
+                           tokens, heads, head_dim, rope_stride);
+    else
+        hipLaunchKernelGGL((rope_half_f32_kernel<1>), grid, dim3(256), 0, stream, x, cosine, sine, out,
+                           tokens, heads, head_dim, rope_stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_half_f16(hipStream_t stream, const uint16_t* x, const float* cosine,
+                                const float* sine, uint16_t* out, uint32_t tokens, uint32_t heads,
+                                uint32_t head_dim, uint32_t rope_stride) {
+    const uint32_t half = head_dim / 2;
+    const bool vec = (half % 4) == 0 && aligned(x, 8) && aligned(out, 8);
+    const uint32_t P = vec ? 4 : 1;
+    const uint64_t threads = static_cast<uint64_t>(tokens) * heads * (half / P);
+    const dim3 grid(static_cast<uint32_t>((threads + 255) / 256));
+    if (vec)
+        hipLaunchKernelGGL((rope_half_f16_kernel<4>), grid, dim3(256), 0, stream, x, cosine, sine, out,
+                           tokens, heads, head_dim, rope_stride);
+    else
+        hipLaunchKernelGGL((rope_half_f16_kernel<1>), grid, dim3(256), 0, stream, x, cosine, sine, out,
+                           tokens, heads, head_dim, rope_stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_interleaved_f32(hipStream_t stream, const float* x, const float* cosine,
+                                       const float* sine, float* out, uint32_t rows,
+                                       uint32_t hidden) {
+    const uint64_t threads = static_cast<uint64_t>(rows) * (hidden / 2);
+    const dim3 grid(static_cast<uint32_t>((threads + 255) / 256));
+    hipLaunchKernelGGL(rope_interleaved_kernel, grid, dim3(256), 0, stream, x, cosine, sine, out, rows,
+                       hidden);
+    return hipGetLastError();
+}
+
+}  // namespace atlas

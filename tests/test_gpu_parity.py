@@ -1,0 +1,333 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Default mode (sequential reduction) must be bit-identical to the oracle for
+every op -- gathers and dequant by construction, norms / RoPE / activations
+because the kernels keep the reference's f32 operation order and share the
+oracle's exp algorithm.  Bit-identity is asserted on the raw bytes; the
+seeded golden cases additionally match the committed SHA-256 digests.
+"""
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import cases
+from atlas_amd import rope_tables_gemma4, rope_tables_llama
+from atlas_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLDEN = json.load(open(os.path.join(HERE, "golden", "golden.json")))["cases"]
+f32 = np.float32
+
+
+def say(msg):
+    print(f"[gpu-parity] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def assert_bits(name, got, exp):
+    assert len(got) == len(exp), name
+    for i, (g, e) in enumerate(zip(got, exp)):
+        g, e = np.asarray(g).reshape(-1), np.asarray(e).reshape(-1)
+        assert g.shape == e.shape, (name, i, g.shape, e.shape)
+        gb, eb = g.view(np.uint8), e.view(np.uint8)
+        if not np.array_equal(gb, eb):
+            gf, ef = g.astype(np.float64), e.astype(np.float64)
+            mism = np.nonzero((g != e) & ~(np.isnan(gf) & np.isnan(ef)))[0]
+            j = mism[0] if mism.size else 0
+            raise AssertionError(f"{name}[{i}]: {mism.size} of {g.size} elements differ; first at {j}: "
+                                 f"gpu={g[j]!r} oracle={e[j]!r} max_abs={np.nanmax(np.abs(gf - ef)):.3e}")
+
+
+def run_golden(rt, ora, name, gpu_fn):
+    build, orc = cases.golden_cases()[name]
+    inp, meta = build()
+    say(f"{name} {meta}")
+    exp = orc(ora, inp, meta)
+    assert cases.digest(exp) == GOLDEN[name]["sha256"], f"oracle drifted from the golden digest for {name}"
+    got = gpu_fn(rt, inp, meta)
+    assert_bits(name, got, exp)
+    assert cases.digest(got) == GOLDEN[name]["sha256"]
+
+
+# ------------------------------------------------------------- golden cases
+
+@pytest.mark.parametrize("name", ["c1_rms_norm", "c3_rms_norm", "c3_rms_residual"])
+def test_golden_rms(rt, ora, name):
+    run_golden(rt, ora, name, cases.rms_gpu)
+
+
+@pytest.mark.parametrize("name", ["c1_swiglu", "c3_geglu"])
+def test_golden_glu(rt, ora, name):
+    run_golden(rt, ora, name, cases.glu_gpu)
+
+
+@pytest.mark.parametrize("name", ["c3_qk_norm_rope_local", "c3_qk_norm_rope_global"])
+def test_golden_qk_norm_rope(rt, ora, name):
+    def gpu(rt_, inp, m):
+        tables = rope_tables_gemma4(inp["pos"], m["rope_stride"], m["head_dim"], m["theta"])
+        return cases.qk_gpu(rt_, inp, m, tables)
+    run_golden(rt, ora, name, gpu)
+
+
+@pytest.mark.parametrize("name", ["c1_rope_q", "c1_rope_k", "c2_rope_f16"])
+def test_golden_rope_half(rt, ora, name):
+    def gpu(rt_, inp, m):
+        return cases.rope_half_gpu(rt_, inp, m, rope_tables_llama(inp["pos"], m["head_dim"], m["theta"]))
+    run_golden(rt, ora, name, gpu)
+
+
+def test_golden_embed_f32(rt, ora):
+    run_golden(rt, ora, "c1_embed_f32", cases.embed_f32_gpu)
+
+
+@pytest.mark.parametrize("name", ["c4_embed_q4_0", "c4_embed_q6_k"])
+def test_golden_embed_quant(rt, ora, name):
+    run_golden(rt, ora, name, cases.embed_q_gpu)
+
+
+def test_golden_ple(rt, ora):
+    run_golden(rt, ora, "c4_ple_q4_0", cases.ple_gpu)
+
+
+def test_golden_f16(rt, ora):
+    run_golden(rt, ora, "c2_add_rms_norm_f16", cases.f16_norm_gpu)
+    run_golden(rt, ora, "c2_swiglu_f16", cases.swiglu_f16_gpu)
+
+
+# ------------------------------------------------- shapes, modes, edge cases
+
+@pytest.mark.parametrize("rows,hidden", [(1, 4), (3, 7), (5, 576), (33, 2048), (256, 1536), (17, 2304), (2, 8192)])
+@pytest.mark.parametrize("mode", ["plain", "residual", "addnorm", "addscale"])
+def test_rms_modes_ragged(rt, ora, rows, hidden, mode):
+    inp, m = cases.rms_case(rows, hidden, 1e-6, 1000 + rows + hidden, mode)
+    say(f"rms {mode} rows={rows} hidden={hidden}")
+    assert_bits(f"rms_{mode}", cases.rms_gpu(rt, inp, m), cases.rms_oracle(ora, inp, m))
+
+
+def test_rms_aliasing_like_reference_call_sites(rt, ora):
+    """gemma4_executor.rs:4492-4506 binds x=work, normalized=work, residual=out=state;
+    :3952 normalises work in place; :4101 adds with out == lhs."""
+    rows, h, eps = 64, 1536, 1e-6
+    inp, m = cases.rms_case(rows, h, eps, 77, "residual")
+    n_exp, out_exp = ora.rms_norm_residual(inp["x"], inp["w"], inp["res"], rows, h, eps)
+    say("rms residual aliased")
+    work, state, w = rt.upload(inp["x"]), rt.upload(inp["res"]), rt.upload(inp["w"])
+    rt.rms_norm_residual(work, w, state, work, state, rows, h, eps)
+    rt.sync()
+    assert_bits("aliased residual", [work.download(rows * h), state.download(rows * h)], [n_exp, out_exp])
+    say("rms in place")
+    work = rt.upload(inp["x"])
+    rt.rms_norm(work, w, work, rows, h, eps)
+    rt.sync()
+    assert_bits("in-place rms", [work.download(rows * h)], [ora.rms_norm(inp["x"], inp["w"], rows, h, eps)])
+    say("add+norm with residual_out == input")
+    a, res = rt.upload(inp["x"]), rt.upload(inp["res"])
+    y = rt.empty(rows * h)
+    rt.add_rms_norm(a, res, w, a, y, rows, h, eps)
+    rt.sync()
+    rs_exp, y_exp = ora.add_rms_norm(inp["x"], inp["res"], inp["w"], rows, h, eps)
+    assert_bits("aliased add+norm", [a.download(rows * h), y.download(rows * h)], [rs_exp, y_exp])
+
+
+def test_rms_unaligned_pointer_takes_scalar_path(rt, ora):
+    rows, h, eps = 9, 1536, 1e-5
+    inp, m = cases.rms_case(rows, h, eps, 78)
+    say("rms unaligned")
+    buf = rt.empty(rows * h + 4)
+    x = buf.offset(4)
+    x.upload(inp["x"])
+    w = rt.upload(inp["w"])
+    y = rt.empty(rows * h + 4).offset(4)
+    rt.rms_norm(x, w, y, rows, h, eps)
+    rt.sync()
+    assert_bits("unaligned rms", [y.download(rows * h)], [ora.rms_norm(inp["x"], inp["w"], rows, h, eps)])
+
+
+def test_reference_fusion_parity_seeds(rt, ora):
+    """The reference's own fused-vs-unfused cases (dispatch_fusion_parity.rs:184-352), LCG inputs."""
+    def lcg_fill(n, state):
+        out = np.empty(n, f32)
+        for i in range(n):
+            state = (state * 1664525 + 1013904223) & 0xFFFFFFFF
+            out[i] = (f32((state >> 8)) / f32(1 << 24) - f32(0.5)) * f32(2.0)
+        return out, state
+
+    state = 0x9E3779B9
+    for hidden in [512, 2048, 2304]:
+        x, state = lcg_fill(hidden, state)
+        w, state = lcg_fill(hidden, state)
+        res, state = lcg_fill(hidden, state)
+        say(f"rms_residual lcg hidden={hidden}")
+        n_exp, out_exp = ora.rms_norm_residual(x, w, res, 1, hidden, 1e-6)
+        xb, wb, rb = rt.upload(x), rt.upload(w), rt.upload(res)
+        nb, ob = rt.empty(hidden), rt.empty(hidden)
+        rt.rms_norm_residual(xb, wb, rb, nb, ob, 1, hidden, 1e-6)
+        rt.sync()
+        assert_bits("lcg residual", [nb.download(hidden), ob.download(hidden)], [n_exp, out_exp])
+    state = 0x853C49E2
+    for count in [256, 2048, 8192]:
+        g, state = lcg_fill(count, state)
+        u, state = lcg_fill(count, state)
+        say(f"geglu lcg count={count}")
+        gb, ub, ob = rt.upload(g), rt.upload(u), rt.empty(count)
+        rt.geglu(gb, ub, ob, count)
+        rt.sync()
+        assert_bits("lcg geglu", [ob.download(count)], [ora.geglu(g, u)])
+
+
+@pytest.mark.parametrize("head_dim,rope_stride,q_heads,has_key", [
+    (256, 128, 8, True), (256, 256, 8, True), (512, 256, 8, True), (128, 64, 4, True), (256, 128, 8, False),
+    (96, 48, 3, True), (64, 32, 2, True)])
+def test_qk_norm_rope_shapes(rt, ora, head_dim, rope_stride, q_heads, has_key):
+    inp, m = cases.qk_case(37, q_heads, head_dim, rope_stride, 1e6, 1e-6, 500 + head_dim, has_key, start=1000)
+    tables = rope_tables_gemma4(inp["pos"], rope_stride, head_dim, 1e6)
+    say(f"qk_norm_rope {m}")
+    assert_bits("qk", cases.qk_gpu(rt, inp, m, tables), cases.qk_oracle(ora, inp, m))
+
+
+def test_qk_norm_rope_in_place_and_decode_positions(rt, ora):
+    d, qh, tokens = 256, 8, 256
+    r = wl.rng(9)
+    q = wl.normal(r, tokens * qh * d)
+    k = wl.normal(r, tokens * d)
+    qw, kw = wl.normal(r, d, 1, 0.1), wl.normal(r, d, 1, 0.1)
+    pos = r.integers(0, 131072, tokens, dtype=np.uint32)
+    c, s = rope_tables_gemma4(pos, 128, 256, 1e4)
+    say("qk in place, decode positions")
+    qb, kb = rt.upload(q), rt.upload(k)
+    rt.qk_norm_rope(qb, kb, rt.upload(qw), rt.upload(kw), rt.upload(c), rt.upload(s), qb, kb, tokens, qh, 1, d, 128,
+                    1e-6)
+    rt.sync()
+    qe, ke = ora.qk_norm_rope(q, k, qw, kw, c, s, tokens, qh, True, d, 128, 1e-6)
+    assert_bits("qk in place", [qb.download(q.size), kb.download(k.size)], [qe, ke])
+
+
+def test_rope_tables_match_oracle_tables(ora):
+    pos = np.array([0, 1, 7, 4095, 131071], np.uint32)
+    for rot, theta in [(256, 1e4), (256, 1e6), (512, 1e6), (128, 1e4)]:
+        a = rope_tables_gemma4(pos, 256, rot, theta)
+        b = ora.rope_tables_gemma4(pos, 256, rot, theta)
+        assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+    a, b = rope_tables_llama(pos, 64, 130000.0), ora.rope_tables_llama(pos, 64, 130000.0)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def test_activations_extremes_and_elementwise(rt, ora):
+    r = wl.rng(21)
+    x = np.concatenate([np.array([-100.0, -17.29969, -1.0, 0.0, 1.0, 17.29969, 100.0, -1e20, 1e20, -88.9, 88.9,
+                                  -104.5, 1e-30, -1e-30], f32), r.uniform(-30, 30, 100003).astype(f32)])
+    y = r.standard_normal(x.size).astype(f32)
+    n = x.size
+    xb, yb, ob = rt.upload(x), rt.upload(y), rt.empty(n)
+    for name, fn, exp in [("silu", lambda: rt.silu(xb, ob, n), ora.silu(x)),
+                          ("gelu", lambda: rt.gelu(xb, ob, n), ora.gelu(x)),
+                          ("swiglu", lambda: rt.swiglu(xb, yb, ob, n), ora.swiglu(x, y)),
+                          ("geglu", lambda: rt.geglu(xb, yb, ob, n), ora.geglu(x, y)),
+                          ("add", lambda: rt.add(xb, yb, ob, n), ora.add(x, y)),
+                          ("multiply", lambda: rt.multiply(xb, yb, ob, n), ora.multiply(x, y)),
+                          ("scale", lambda: rt.scale(xb, f32(39.191837), ob, n), ora.scale(x, f32(39.191837)))]:
+        say(f"elementwise {name} n={n}")
+        fn()
+        rt.sync()
+        assert_bits(name, [ob.download(n)], [exp])
+
+
+def test_geglu_offset_ple_slices(rt, ora):
+    r = wl.rng(22)
+    rows, layers, width = 64, 35, 256
+    gate = wl.normal(r, rows * width)
+    ple = wl.normal(r, rows * layers * width)
+    gb, pb, ob = rt.upload(gate), rt.upload(ple), rt.empty(rows * width)
+    for layer in (0, 17, 34):
+        say(f"geglu_offset layer={layer}")
+        rt.geglu_offset(gb, pb, ob, layer * width, layers * width, width, rows)
+        rt.sync()
+        assert_bits("geglu_offset", [ob.download(rows * width)],
+                    [ora.geglu_offset(gate, ple, layer * width, layers * width, width, rows)])
+
+
+def test_groups_stable(rt, ora):
+    r = wl.rng(23)
+    width, groups = 256, 35 * 64
+    v = wl.normal(r, (groups, width))
+    v[5] = 0.0
+    v[9] *= f32(1e30)
+    w = wl.normal(r, width, 1, 0.1)
+    say("groups stable")
+    vb = rt.upload(v)
+    rt.rms_norm_groups_stable(vb, rt.upload(w), width, groups, 1e-6)
+    rt.sync()
+    assert_bits("groups", [vb.download(v.size)], [ora.rms_norm_groups_stable(v, w, width, groups, 1e-6)])
+
+
+def test_full_size_gathers_c4(rt, ora):
+    S = wl.QuantGatherShape()
+    for q6 in (False, True):
+        inp, m = cases.embed_q_case(S.vocab, S.hidden, S.tokens, 600 + q6, q6)
+        inp["ids"][:4] = [0, S.vocab - 1, S.vocab - 1, 0]      # boundary rows, repeated ids
+        say(f"embed full vocab q6={q6}")
+        assert_bits("embed", cases.embed_q_gpu(rt, inp, m), cases.embed_q_oracle(ora, inp, m))
+
+
+def test_full_size_ple_c4(rt, ora):
+    S = wl.QuantGatherShape()
+    inp, m = cases.ple_case(S.vocab, S.ple_layers, S.ple_width, S.tokens, 610, False)
+    say("ple full size q4_0")
+    assert_bits("ple", cases.ple_gpu(rt, inp, m), cases.ple_oracle(ora, inp, m))
+    inp, m = cases.ple_case(4096, S.ple_layers, S.ple_width, 1024, 611, True)
+    say("ple q6_k")
+    assert_bits("ple q6", cases.ple_gpu(rt, inp, m), cases.ple_oracle(ora, inp, m))
+
+
+def test_out_of_range_ids_follow_reference(rt, ora):
+    vocab, h, t = 100, 512, 6
+    ids = np.array([1, 100, 5, 4000000000, 99, 0], np.uint32)
+    for q6 in (False, True):
+        inp, m = cases.embed_q_case(vocab, h, t, 620, q6)
+        inp["ids"] = ids
+        say(f"out-of-range ids q6={q6}")
+        tb, ib = rt.upload(inp["table"]), rt.upload(ids)
+        sentinel = np.full(t * h, 7.0, f32)
+        ob = rt.upload(sentinel)
+        (rt.embed_q6_k if q6 else rt.embed_q4_0)(tb, ib, ob, vocab, h, t, m["scale"])
+        rt.sync()
+        exp = (ora.embed_q6_k if q6 else ora.embed_q4_0)(inp["table"], ids, vocab, h, m["scale"], out=sentinel)
+        assert_bits("oob untouched", [ob.download(t * h)], [exp])
+    table = wl.normal(wl.rng(1), vocab * h)
+    tb, ib, ob = rt.upload(table), rt.upload(ids), rt.empty(t * h)
+    rt.embed_f32(tb, ib, ob, vocab, h, t)
+    rt.sync()
+    assert_bits("oob f32 zeros", [ob.download(t * h)], [ora.embed_f32(table, ids, vocab, h)])
+
+
+def test_wide_reduction_is_tolerance_level(rt, ora):
+    """ATLAS_REDUCTION_WIDE reorders the sum of squares: plain RMSNorm stays
+    within 1e-5 relative per element; epilogues that cancel are checked
+    normwise (1e-6) since an elementwise bound is not meaningful there."""
+    from atlas_amd import ATLAS_REDUCTION_SEQUENTIAL, ATLAS_REDUCTION_WIDE
+    rows, h, eps = 512, 1536, 1e-6
+    inp, m = cases.rms_case(rows, h, eps, 91)
+    rt.set_reduction(ATLAS_REDUCTION_WIDE)
+    try:
+        say("wide rms")
+        got = cases.rms_gpu(rt, inp, m)[0]
+        exp = cases.rms_oracle(ora, inp, m)[0]
+        assert np.max(np.abs(got - exp) / np.abs(exp)) <= 1e-5
+        m2 = dict(m, mode="residual")
+        got_n, got_o = cases.rms_gpu(rt, inp, m2)
+        exp_n, exp_o = cases.rms_oracle(ora, inp, m2)
+        assert np.max(np.abs(got_n - exp_n) / np.abs(exp_n)) <= 1e-5
+        assert np.linalg.norm(got_o - exp_o) / np.linalg.norm(exp_o) <= 1e-6
+        qinp, qm = cases.qk_case(64, 8, 256, 128, 1e4, 1e-6, 92)
+        tables = rope_tables_gemma4(qinp["pos"], 128, 256, 1e4)
+        say("wide qk")
+        gq = cases.qk_gpu(rt, qinp, qm, tables)
+        eq = cases.qk_oracle(ora, qinp, qm)
+        for g_, e_ in zip(gq, eq):
+            assert np.linalg.norm(g_ - e_) / np.linalg.norm(e_) <= 1e-6
+    finally:
+        rt.set_reduction(ATLAS_REDUCTION_SEQUENTIAL)

@@ -1,0 +1,402 @@
+"""Pin the CPU oracle before it is trusted as the parity checker.
+
+Each oracle function is checked against the reference's own known-answer
+values (tests/golden/kats.json, transcribed from the reference tests), and
+against what mathematics fixes: float64 evaluations, closed forms,
+invariants and exhaustive / brute-force sweeps.  The checks are chosen so a
+plausible mistake (dropped epsilon, wrong divisor, swapped pair, wrong nibble
+or scale index, missing rounding step) fails at least one of them.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KATS = json.load(open(os.path.join(HERE, "golden", "kats.json")))
+f32 = np.float32
+
+
+def ulp_err(actual, exact):
+    actual = np.asarray(actual, np.float64)
+    exact = np.asarray(exact, np.float64)
+    spacing = np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64)
+    return np.abs(actual - exact) / spacing
+
+
+# --------------------------------------------------------------------- f16
+
+def test_f16_decode_exhaustive(ora):
+    codes = np.arange(65536, dtype=np.uint16)
+    got = ora.f16_to_f32(codes)
+    ref = codes.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f16_encode_is_ieee_rne(ora):
+    r = np.random.default_rng(7)
+    vals = np.concatenate([
+        r.standard_normal(200000).astype(f32) * f32(100),
+        r.uniform(-70000, 70000, 20000).astype(f32),
+        (r.standard_normal(20000) * 1e-6).astype(f32),          # f16 subnormal range
+        np.array([0.0, -0.0, 65504.0, 65519.0, 65520.0, 1e9, -1e9, np.inf, -np.inf,
+                  2.0 ** -24, 2.0 ** -25, 1.5 * 2.0 ** -25, 1.0009765625 + 2.0 ** -11], f32),
+    ])
+    got = ora.f32_to_f16(vals)
+    ref = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+    # Atlas's converter rounds 1.9999999 to 1.0 (carry bug); IEEE RNE gives 2.0.
+    assert ora.f32_to_f16(np.array([1.9999999], f32))[0] == 0x4000
+
+
+# --------------------------------------------------------------- exp / act
+
+def test_expf_faithful_against_float64(ora):
+    r = np.random.default_rng(3)
+    xs = np.concatenate([r.uniform(-87, 88, 30000), r.uniform(-1, 1, 10000),
+                         np.array([0.0, 1.0, -1.0, 0.5, -0.5, 88.0, -87.0])]).astype(f32)
+    got = ora.expf(xs)
+    err = ulp_err(got, np.exp(xs.astype(np.float64)))
+    assert err.max() < 1.0, err.max()
+    assert ora.expf(np.array([0.0], f32))[0] == 1.0
+    assert np.isinf(ora.expf(np.array([89.5], f32))[0])
+    assert ora.expf(np.array([-105.0], f32))[0] == 0.0
+    sub = ora.expf(np.array([-100.0], f32))[0]            # subnormal result
+    assert 0 < sub < np.finfo(np.float32).tiny
+    assert abs(float(sub) - np.exp(-100.0)) <= 2.0 ** -149
+
+
+def test_tanh_silu_against_float64(ora):
+    lib = ora.lib()
+    r = np.random.default_rng(5)
+    xs = np.concatenate([r.uniform(-12, 12, 20000), r.uniform(-0.01, 0.01, 2000)]).astype(f32)
+    t = np.array([lib.oracle_tanhf(float(x)) for x in xs], np.float64)
+    assert np.max(np.abs(t - np.tanh(xs.astype(np.float64)))) < 2.5e-7
+    s = ora.silu(xs).astype(np.float64)
+    x64 = xs.astype(np.float64)
+    exact = x64 / (1.0 + np.exp(-x64))
+    assert ulp_err(s, exact).max() <= 4.0
+    assert ora.silu(np.array([-200.0], f32))[0] == 0.0
+
+
+def test_gelu_reference_extremes_and_formula(ora):
+    kat = KATS["gelu_extremes"]
+    x = np.array(kat["input"], f32)
+    got = ora.gelu(x)
+    assert np.all(np.isfinite(got))
+    # phase_00_bootstrap.rs:137-141: CPU tanh formula, abs <= 1e-5
+    a = f32(0.7978846) * (x + f32(0.044715) * x * x * x)
+    exp_cpu = (f32(0.5) * x * (f32(1.0) + np.tanh(a))).astype(f32)
+    assert np.max(np.abs(got - exp_cpu)) <= kat["tolerance"]
+    r = np.random.default_rng(11)
+    xs = r.uniform(-8, 8, 50000).astype(f32)
+    x64 = xs.astype(np.float64)
+    exact = 0.5 * x64 * (1 + np.tanh(0.7978845608 * (x64 + 0.044715 * x64 ** 3)))
+    assert np.max(np.abs(ora.gelu(xs) - exact)) < 2e-6
+    # the inf guard: x large negative -> 0, large positive -> x
+    assert ora.gelu(np.array([-1e20], f32))[0] == 0.0
+    assert ora.gelu(np.array([1e20], f32))[0] == f32(1e20)
+
+
+def test_glu_is_activation_times_up(ora):
+    r = np.random.default_rng(2)
+    g, u = r.standard_normal(4096).astype(f32), r.standard_normal(4096).astype(f32)
+    assert np.array_equal(ora.swiglu(g, u), ora.silu(g) * u)
+    assert np.array_equal(ora.geglu(g, u), ora.gelu(g) * u)
+    ple = r.standard_normal((3, 5 * 64)).astype(f32)
+    gate = r.standard_normal((3, 64)).astype(f32)
+    got = ora.geglu_offset(gate, ple, 2 * 64, 5 * 64, 64, 3).reshape(3, 64)
+    assert np.array_equal(got, ora.gelu(gate).reshape(3, 64) * ple[:, 128:192])
+
+
+# ----------------------------------------------------------------- RMSNorm
+
+def rms_f64(x, w, eps):
+    x64 = x.astype(np.float64)
+    inv = 1.0 / np.sqrt(np.mean(x64 * x64, axis=-1, keepdims=True) + eps)
+    return x64 * inv * w.astype(np.float64)
+
+
+def test_rms_norm_reference_kat(ora):
+    k = KATS["rms_norm"]
+    x, w = np.array(k["input"], f32), np.array(k["weight"], f32)
+    got = ora.rms_norm(x, w, k["rows"], k["hidden"], k["epsilon"]).reshape(2, 4)
+    exact = rms_f64(x.reshape(2, 4), w, k["epsilon"])
+    assert np.max(np.abs(got - exact)) <= k["tolerance"]
+    assert np.max(np.abs(got - exact) / np.abs(exact)) < 1e-6
+
+
+def test_rms_norm_math_and_invariants(ora):
+    r = np.random.default_rng(4)
+    rows, h = 64, 1536
+    x = r.standard_normal((rows, h)).astype(f32)
+    w = (1 + 0.1 * r.standard_normal(h)).astype(f32)
+    y = ora.rms_norm(x, w, rows, h, 1e-6).reshape(rows, h)
+    assert np.max(np.abs(y - rms_f64(x, w, 1e-6)) / np.abs(rms_f64(x, w, 1e-6))) < 5e-6
+    # scale invariance (eps negligible) and unit RMS of y / w
+    y2 = ora.rms_norm(x * f32(8), w, rows, h, 1e-6).reshape(rows, h)
+    assert np.max(np.abs(y2 - y) / np.abs(y)) < 1e-5
+    assert np.allclose(np.sqrt(np.mean((y / w).astype(np.float64) ** 2, axis=1)), 1.0, atol=1e-5)
+    # sequential f32 fold: equal to a float32 cumulative sum in index order
+    sq = (x * x).astype(f32)
+    seq = np.cumsum(sq, axis=1, dtype=np.float32)[:, -1]
+    lib = ora.lib()
+    for i in range(4):
+        row = np.ascontiguousarray(x[i])
+        inv = lib.oracle_inverse_rms(row.ctypes.data, h, f32(1e-6))
+        assert inv == f32(1) / np.sqrt(seq[i] / f32(h) + f32(1e-6))
+
+
+def test_fused_epilogues_equal_unfused_chains(ora):
+    r = np.random.default_rng(9)
+    rows, h, eps = 16, 1536, 1e-6
+    x = r.standard_normal(rows * h).astype(f32)
+    w = (1 + 0.1 * r.standard_normal(h)).astype(f32)
+    res = r.standard_normal(rows * h).astype(f32)
+    n = ora.rms_norm(x, w, rows, h, eps)
+    # post-norm residual epilogue == rms_norm then vector_add
+    nn, out = ora.rms_norm_residual(x, w, res, rows, h, eps)
+    assert np.array_equal(nn, n) and np.array_equal(out, res + n)
+    # pre-norm add + norm == vector_add then rms_norm
+    rs, y = ora.add_rms_norm(x, res, w, rows, h, eps)
+    assert np.array_equal(rs, x + res)
+    assert np.array_equal(y, ora.rms_norm(x + res, w, rows, h, eps))
+    # PLE epilogue == norm, add, scale
+    st = ora.rms_norm_add_scale(x, w, res, f32(0.37), rows, h, eps)
+    assert np.array_equal(st, ((res + n) * f32(0.37)).astype(f32))
+
+
+def test_groups_stable(ora):
+    r = np.random.default_rng(12)
+    width, groups = 256, 20
+    v = r.standard_normal((groups, width)).astype(f32)
+    v[3] = 0.0
+    v[5] *= f32(1e30)   # x*x would overflow without the max scaling
+    w = (1 + 0.1 * r.standard_normal(width)).astype(f32)
+    got = ora.rms_norm_groups_stable(v, w, width, groups, 1e-6).reshape(groups, width)
+    assert np.all(got[3] == 0.0)
+    assert np.all(np.isfinite(got))
+    exact = rms_f64(v.astype(np.float64), w, 1e-6)
+    ok = np.arange(groups) != 3
+    assert np.max(np.abs(got[ok] - exact[ok]) / np.maximum(np.abs(exact[ok]), 1e-30)) < 5e-6
+
+
+def test_f16_norms_are_widen_compute_round(ora):
+    r = np.random.default_rng(13)
+    rows, h = 8, 2048
+    x = r.standard_normal(rows * h).astype(np.float16).view(np.uint16)
+    res = r.standard_normal(rows * h).astype(np.float16).view(np.uint16)
+    w = (1 + 0.1 * r.standard_normal(h)).astype(np.float16).view(np.uint16)
+    got = ora.rms_norm_f16(x, w, rows, h, 1e-5)
+    ref = ora.f32_to_f16(ora.rms_norm(ora.f16_to_f32(x), ora.f16_to_f32(w), rows, h, 1e-5))
+    assert np.array_equal(got, ref)
+    rs, y = ora.add_rms_norm_f16(x, res, w, rows, h, 1e-5)
+    stored = ora.f32_to_f16(ora.f16_to_f32(x) + ora.f16_to_f32(res))
+    assert np.array_equal(rs, stored)
+    assert np.array_equal(y, ora.f32_to_f16(ora.rms_norm(ora.f16_to_f32(stored), ora.f16_to_f32(w), rows, h, 1e-5)))
+    g = r.standard_normal(4096).astype(np.float16).view(np.uint16)
+    u = r.standard_normal(4096).astype(np.float16).view(np.uint16)
+    assert np.array_equal(ora.swiglu_f16(g, u), ora.f32_to_f16(ora.swiglu(ora.f16_to_f32(g), ora.f16_to_f32(u))))
+
+
+# -------------------------------------------------------------------- RoPE
+
+def test_rope_reference_kat(ora):
+    k = KATS["rope"]
+    x = np.array(k["input"], f32)
+    c, s = np.array(k["cos"], f32), np.array(k["sin"], f32)
+    got = ora.rope_interleaved(x, k["rows"], k["hidden"], c, s)
+    x64 = x.reshape(2, 2, 2).astype(np.float64)
+    exp = np.stack([x64[..., 0] * c - x64[..., 1] * s, x64[..., 0] * s + x64[..., 1] * c], -1).reshape(-1)
+    assert np.max(np.abs(got - exp)) <= k["tolerance"]
+
+
+def test_rope_angle_kats(ora):
+    k = KATS["rope_angle"]
+    n = k["normal"]
+    assert ora.rope_angle(n["position"], n["pair"], n["rotary"], n["theta"], n["factor"]) == n["expected"]
+    sp = k["suppressed"]
+    assert abs(ora.rope_angle(sp["position"], sp["pair"], sp["rotary"], sp["theta"], sp["factor"])) < sp["abs_below"]
+    o = k["outside_partial_width"]
+    assert ora.rope_angle(o["position"], o["pair"], o["rotary"], o["theta"], o["factor"]) == o["expected"]
+    c, s = ora.rope_tables_gemma4(np.array([0, 8], np.uint32), 128, 256, 1e6)
+    assert np.all(c[0] == 1.0) and np.all(s[0] == 0.0)
+    assert c[1, 0] == np.float32(np.cos(np.float32(8.0)))
+    c2, s2 = ora.rope_tables_llama(np.array([0, 5], np.uint32), 64, 1e4)
+    assert np.all(c2[0] == 1.0) and np.all(s2[0] == 0.0)
+
+
+def test_rope_half_equals_reference_three_kernel_chain(ora):
+    """rope_half_to_interleaved -> rope_f32 -> rope_interleaved_to_half (kernels.metal:940-994)."""
+    r = np.random.default_rng(14)
+    tokens, heads, d = 5, 3, 64
+    x = r.standard_normal((tokens, heads, d)).astype(f32)
+    c, s = ora.rope_tables_llama(np.arange(tokens, dtype=np.uint32) * 7, d, 130000.0)
+    got = ora.rope_half(x, c, s, tokens, heads, d, d // 2).reshape(tokens, heads, d)
+    for t in range(tokens):
+        inter = np.empty((heads, d), f32)
+        inter[:, 0::2], inter[:, 1::2] = x[t, :, : d // 2], x[t, :, d // 2:]
+        rot = ora.rope_interleaved(inter, heads, d, c[t], s[t]).reshape(heads, d)
+        back = np.concatenate([rot[:, 0::2], rot[:, 1::2]], axis=1)
+        assert np.array_equal(got[t], back)
+    # pair norm preserved; identity at position 0
+    n_in = x[..., : d // 2] ** 2 + x[..., d // 2:] ** 2
+    n_out = got[..., : d // 2] ** 2 + got[..., d // 2:] ** 2
+    assert np.allclose(n_in, n_out, rtol=1e-5)
+    assert np.array_equal(got[0], x[0])
+
+
+def test_qk_norm_rope_equals_norm_then_rope(ora):
+    r = np.random.default_rng(15)
+    tokens, qh, d, eps = 6, 8, 256, 1e-6
+    q = r.standard_normal((tokens, qh, d)).astype(f32)
+    k = r.standard_normal((tokens, 1, d)).astype(f32)
+    qw = (1 + 0.1 * r.standard_normal(d)).astype(f32)
+    kw = (1 + 0.1 * r.standard_normal(d)).astype(f32)
+    c, s = ora.rope_tables_gemma4(np.arange(tokens, dtype=np.uint32) + 100, 128, 256, 1e4)
+    qo, ko = ora.qk_norm_rope(q, k, qw, kw, c, s, tokens, qh, True, d, 128, eps)
+    qn = ora.rms_norm(q.reshape(-1, d), qw, tokens * qh, d, eps)
+    kn = ora.rms_norm(k.reshape(-1, d), kw, tokens, d, eps)
+    assert np.array_equal(qo, ora.rope_half(qn, c, s, tokens, qh, d, 128))
+    assert np.array_equal(ko, ora.rope_half(kn, c, s, tokens, 1, d, 128))
+
+
+# ---------------------------------------------------------- dequant/gathers
+
+def test_q4_0_reference_kat(ora):
+    k = KATS["q4_0"]
+    block = np.zeros(18, np.uint8)
+    block[0:2] = np.array([k["scale_bits"]], np.uint16).view(np.uint8)
+    for i in range(16):
+        block[2 + i] = (i & 15) | ((15 - i) << 4)
+    got = ora.dequant_q4_0_block(block)
+    for i in range(16):
+        assert got[i] == i - 8.0 and got[i + 16] == 7.0 - i
+
+
+def _q6k_kat_block():
+    b = np.zeros(210, np.uint8)
+    b[208:210] = np.array([0x3800], np.uint16).view(np.uint8)
+    for index in range(256):
+        value = index % 64
+        half, within = index // 128, index % 128
+        stream, lane = within // 32, within % 32
+        ql = half * 64 + lane + (32 if stream % 2 == 1 else 0)
+        b[ql] |= ((value & 0x0F) << 4) if stream >= 2 else (value & 0x0F)
+        b[128 + half * 32 + lane] |= ((value >> 4) & 3) << (stream * 2)
+    b[192:208] = 1
+    return b
+
+
+def test_q6_k_reference_kat_and_independent_decoder(ora):
+    k = KATS["q6_k"]
+    b = _q6k_kat_block()
+    got = ora.dequant_q6_k_block(b)
+    for idx, val in k["expected"].items():
+        assert got[int(idx)] == val
+    assert np.array_equal(got, ora.dequant_q6_k_block(b, llama_order=True))
+    # the KAT layout encodes value = index % 64 -> (code - 32) * 1 * 0.5
+    assert np.array_equal(got, ((np.arange(256) % 64) - 32).astype(f32) * f32(0.5))
+    r = np.random.default_rng(16)
+    for _ in range(200):
+        blk = np.frombuffer(r.bytes(210), np.uint8).copy()
+        blk[208:210] = np.array([np.float16(r.uniform(1e-4, 1))]).view(np.uint8)
+        assert np.array_equal(ora.dequant_q6_k_block(blk), ora.dequant_q6_k_block(blk, llama_order=True))
+
+
+def test_dequant_brute_force_every_code(ora):
+    r = np.random.default_rng(17)
+    for d in [np.float16(1.0), np.float16(0.0137), np.float16(-2.5), np.float16(6e-5)]:
+        for nib in range(16):
+            block = np.zeros(18, np.uint8)
+            block[0:2] = np.array([d]).view(np.uint8)
+            block[2:] = nib | (nib << 4)
+            got = ora.dequant_q4_0_block(block)
+            assert np.all(got == np.float64(nib - 8) * np.float64(d))  # exact in f32
+    for _ in range(20):
+        d = np.float16(r.uniform(-1, 1))
+        sc = int(r.integers(-128, 128))
+        for code in range(64):
+            b = np.zeros(210, np.uint8)
+            b[208:210] = np.array([d]).view(np.uint8)
+            b[192:208] = np.array([sc], np.int8).view(np.uint8)[0]
+            low, high = code & 15, code >> 4
+            b[0:64] = low | (low << 4)
+            b[64:128] = low | (low << 4)
+            b[128:192] = high | (high << 2) | (high << 4) | (high << 6)
+            got = ora.dequant_q6_k_block(b)
+            assert np.all(got == np.float64(code - 32) * sc * np.float64(d))
+
+
+def test_embedding_kat_and_gathers(ora):
+    k = KATS["embedding"]
+    got = ora.embed_f32(np.array(k["table"], f32), np.array(k["ids"], np.uint32), k["vocab"], k["hidden"])
+    assert np.max(np.abs(got - np.array(k["expected"], f32))) <= k["tolerance"]
+    assert np.array_equal(got, np.array(k["expected"], f32))  # a gather is a copy
+    zero = ora.embed_f32(np.array(k["table"], f32), np.array([7], np.uint32), 3, 4)
+    assert np.all(zero == 0.0)
+    from atlas_amd import workloads as wl
+    r = wl.rng(18)
+    vocab, h, t = 64, 512, 9
+    for q6 in (False, True):
+        table = wl.q6_k_table(r, vocab, h) if q6 else wl.q4_0_table(r, vocab, h)
+        ids = wl.token_ids(r, t, vocab)
+        ids[2] = vocab + 5  # untouched row
+        scale = wl.f32_sqrt(h)
+        fn = ora.embed_q6_k if q6 else ora.embed_q4_0
+        sentinel = np.full(t * h, 123.0, f32)
+        got = fn(table, ids, vocab, h, scale, out=sentinel).reshape(t, h)
+        rb = wl.q_row_bytes(h, q6)
+        qk, bb = (256, 210) if q6 else (32, 18)
+        for i, tok in enumerate(ids):
+            if tok >= vocab:
+                assert np.all(got[i] == 123.0)
+                continue
+            row = table[tok * rb:(tok + 1) * rb]
+            deq = np.concatenate([
+                (ora.dequant_q6_k_block if q6 else ora.dequant_q4_0_block)(row[b * bb:(b + 1) * bb])
+                for b in range(h // qk)])
+            assert np.array_equal(got[i], deq * scale)
+
+
+def test_ple_combine_kat_and_chain(ora):
+    k = KATS["ple_combine"]
+    got = ora.combine_ple(np.array(k["identity"], f32), np.array(k["context"], f32))
+    exp = np.array([6 / np.sqrt(2), -2 / np.sqrt(2)])
+    assert np.max(np.abs(got - exp)) < k["tolerance"]
+    from atlas_amd import workloads as wl
+    assert np.float32(0.70710677) == wl.SQRT_2_RECIP
+    r = wl.rng(19)
+    vocab, layers, width, t = 32, 3, 256, 5
+    for q6 in (False, True):
+        table = wl.q6_k_table(r, vocab, layers * width) if q6 else wl.q4_0_table(r, vocab, layers * width)
+        ids = wl.token_ids(r, t, vocab)
+        proj = wl.normal(r, (t, layers, width))
+        got = ora.ple(table, ids, proj, vocab, layers, width, f32(16.0), wl.SQRT_2_RECIP, q6=q6)
+        lookup = (ora.embed_q6_k if q6 else ora.embed_q4_0)(table, ids, vocab, layers * width, 1.0)
+        chain = ora.combine_ple(ora.scale(lookup, f32(16.0)), proj.reshape(-1))
+        assert np.array_equal(got, chain)
+
+
+# ------------------------------------------------- planted-mistake controls
+
+def test_pins_catch_planted_mistakes(ora):
+    """Run the same pins against deliberately wrong CPU variants; each must fail."""
+    k = KATS["rms_norm"]
+    x, w = np.array(k["input"], f32).reshape(2, 4), np.array(k["weight"], f32)
+    exact = rms_f64(x, w, k["epsilon"])
+    wrong_div = x / np.sqrt(np.sum(x * x, 1, keepdims=True) / 3 + f32(1e-5)) * w   # h-1 divisor
+    assert np.max(np.abs(wrong_div - exact)) > k["tolerance"]
+    kr = KATS["rope"]
+    xr = np.array(kr["input"], f32).reshape(2, 2, 2)
+    c, s = np.array(kr["cos"], f32), np.array(kr["sin"], f32)
+    good = ora.rope_interleaved(xr, 2, 4, c, s)
+    swapped_sign = np.stack([xr[..., 0] * c + xr[..., 1] * s, xr[..., 0] * s - xr[..., 1] * c], -1).reshape(-1)
+    assert np.max(np.abs(good - swapped_sign)) > kr["tolerance"]
+    b = _q6k_kat_block()
+    wrong_scale_index = b.copy()
+    wrong_scale_index[192] = 2  # scale of group 0 only: a wrong index must change values
+    assert not np.array_equal(ora.dequant_q6_k_block(b), ora.dequant_q6_k_block(wrong_scale_index))
