@@ -2,8 +2,10 @@
 //
 // Every kernel translation unit is compiled with -ffp-contract=off and without
 // fast-math, so each `a * b + c` below is two IEEE-rounded operations, exactly
-// as the reference's Rust CPU operators evaluate them.  Division and sqrt use
-// HIP's default correctly-rounded binary32 lowering (__fdiv_rn / __fsqrt_rn).
+// as the reference's Rust CPU operators evaluate them.  Division and square
+// root must be correctly rounded as well (Rust's f32 `/` and `sqrt`): see
+// fdiv_rn / sqrt_rn.  (HIP's __fsqrt_rn maps to the native ~1 ulp v_sqrt_f32
+// unless OCML rounded operations are enabled, so it is not used.)
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -12,6 +14,14 @@
 namespace atlas {
 
 constexpr int kWave = 64;  // CDNA wavefront width
+
+// IEEE binary32 division, correctly rounded: HIP's default lowering of '/'
+// (v_div_scale / v_rcp / Newton steps / v_div_fmas / v_div_fixup).
+__device__ __forceinline__ float fdiv_rn(float a, float b) { return a / b; }
+
+// IEEE binary32 square root, correctly rounded.  llvm.sqrt.f32 under HIP's
+// default -fhip-fp32-correctly-rounded-divide-sqrt.
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
 
 __device__ __forceinline__ float pow2i(int k) {  // 2^k, k in [-126, 127]
     return __uint_as_float(static_cast<uint32_t>(k + 127) << 23);
@@ -51,11 +61,11 @@ __device__ __forceinline__ float tanh_f32(float v) {
     if (v >= 10.0f) return 1.0f;
     if (v <= -10.0f) return -1.0f;
     float e = exp_f32(2.0f * v);
-    return __fdiv_rn(e - 1.0f, e + 1.0f);
+    return fdiv_rn(e - 1.0f, e + 1.0f);
 }
 
 // x / (1 + e^-x)   (kernels.metal:27-36)
-__device__ __forceinline__ float silu_f32(float x) { return __fdiv_rn(x, 1.0f + exp_f32(-x)); }
+__device__ __forceinline__ float silu_f32(float x) { return fdiv_rn(x, 1.0f + exp_f32(-x)); }
 
 // tanh-GELU with the overflow guard (kernels.metal:752-767):
 // a = c0*(x + ((c1*x)*x)*x); inf(a) -> (a > 0 ? x : 0); else (0.5*x)*(1 + tanh(a)).
@@ -68,7 +78,7 @@ __device__ __forceinline__ float gelu_tanh_f32(float x) {
 // 1 / sqrt(mean + eps) with the CPU operators' two roundings
 // (phase_02_operators.rs:233-235: `.sqrt().recip()`).
 __device__ __forceinline__ float inverse_rms(float sum, float hidden, float epsilon) {
-    return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(sum, hidden) + epsilon));
+    return fdiv_rn(1.0f, sqrt_rn(fdiv_rn(sum, hidden) + epsilon));
 }
 
 __device__ __forceinline__ float h2f(uint16_t bits) {

@@ -281,7 +281,7 @@ __global__ __launch_bounds__(64) void groups_stable_kernel(float* values, const 
     }
     float partial = 0.0f;
     for (uint32_t i = lane; i < width; i += kWave) {
-        float scaled = __fdiv_rn(v[i], m);
+        float scaled = fdiv_rn(v[i], m);
         float s2 = scaled * scaled;
         if (sequential)
             sq[i] = s2;
@@ -302,8 +302,8 @@ __global__ __launch_bounds__(64) void groups_stable_kernel(float* values, const 
     } else {
         sum = wave_sum(partial);
     }
-    const float root = __fsqrt_rn(__fdiv_rn(sum, static_cast<float>(width)) + __fdiv_rn(epsilon, m * m));
-    const float inv = __fdiv_rn(__fdiv_rn(1.0f, root), m);
+    const float root = sqrt_rn(fdiv_rn(sum, static_cast<float>(width)) + fdiv_rn(epsilon, m * m));
+    const float inv = fdiv_rn(fdiv_rn(1.0f, root), m);
     for (uint32_t i = lane; i < width; i += kWave) v[i] = v[i] * inv * weight[i];
 }
 
