@@ -564,8 +564,9 @@ static int ple(atlas_hip_ctx* ctx, int q6, const uint8_t* table, const uint32_t*
     const uint64_t row = static_cast<uint64_t>(layers) * width;
     const uint32_t qk = q6 ? 256 : 32;
     if (!table || !ids || !projection || !output) return invalid(ctx, "PLE buffer is null");
-    if (layers == 0 || width == 0 || tokens == 0 || row % qk != 0 || row > 65536 * 4)
+    if (layers == 0 || width == 0 || tokens == 0 || row % qk != 0)
         return invalid(ctx, "PLE dimensions are invalid");
+    if (row > 16384) return invalid(ctx, "PLE rows are limited to 16384 values (layers * width)");
     if (!aligned16(projection) || !aligned16(output)) return invalid(ctx, "PLE projection/output must be 16-byte aligned");
     return launched(ctx,
                     atlas::launch_ple_quant(ctx->stream, q6, table, ids, projection, output, vocab, layers, width,

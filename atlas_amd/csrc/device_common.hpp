@@ -28,11 +28,13 @@ __device__ __forceinline__ float pow2i(int k) {  // 2^k, k in [-126, 127]
 }
 
 // binary32 exp: Cody & Waite reduction x = n*ln2 + r (ln2 split into the
-// 9-bit head 355/512 and its tail so n*head is exact) followed by the
-// degree-7 Taylor polynomial of e^r on |r| <= ln2/2, evaluated in Horner form.
-// Uses only IEEE add/sub/mul, floor and exponent-field assembly, so the
-// result is a deterministic function of x (faithfully rounded: < 1 ulp
-// against float64 exp over the finite range).
+// 9-bit head 355/512 and its tail so n*head is exact), then the degree-7
+// Taylor polynomial of e^r on |r| <= ln2/2 in Horner form with fused
+// multiply-adds (each step one IEEE fma, correctly rounded), and the 2^n
+// scale assembled in the exponent field.  Every step is an IEEE operation
+// (fma, floor, exact power-of-two multiply), so the CPU oracle's restatement
+// with C99 fmaf gives the same bits; the result is faithfully rounded
+// (< 1 ulp against float64 exp over the finite range).
 __device__ __forceinline__ float exp_f32(float x) {
     if (x != x) return x;
     if (x > 89.0f) return __builtin_inff();
@@ -40,16 +42,17 @@ __device__ __forceinline__ float exp_f32(float x) {
     const float log2e = 1.44269502162933349609375f;
     const float ln2_hi = 0.693359375f;
     const float ln2_lo = -2.12194440e-4f;
-    float fn = floorf(x * log2e + 0.5f);
-    int n = static_cast<int>(fn);
-    float r = (x - fn * ln2_hi) - fn * ln2_lo;
-    float poly = 1.0f / 5040.0f;
-    poly = 1.0f / 720.0f + r * poly;
-    poly = 1.0f / 120.0f + r * poly;
-    poly = 1.0f / 24.0f + r * poly;
-    poly = 1.0f / 6.0f + r * poly;
-    poly = 0.5f + r * poly;
-    float p = 1.0f + (r + (r * r) * poly);
+    const float fn = floorf(__builtin_fmaf(x, log2e, 0.5f));
+    const int n = static_cast<int>(fn);
+    const float r = __builtin_fmaf(-fn, ln2_lo, __builtin_fmaf(-fn, ln2_hi, x));
+    float p = 1.0f / 5040.0f;
+    p = __builtin_fmaf(p, r, 1.0f / 720.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 120.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 24.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 6.0f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
     if (n > 127) return (p * pow2i(127)) * pow2i(n - 127);
     if (n < -126) return (p * pow2i(n + 100)) * pow2i(-100);
     return p * pow2i(n);
@@ -85,8 +88,17 @@ __device__ __forceinline__ float h2f(uint16_t bits) {
     return static_cast<float>(__builtin_bit_cast(_Float16, bits));
 }
 
-__device__ __forceinline__ uint16_t f2h(float v) {  // IEEE RNE
-    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+// Materialise an f32 value in a VGPR.  The empty asm (register constraint
+// only, no instruction) stops instruction selection from folding the
+// producing multiply into the f32 -> f16 conversion (v_fma_mix*_f16 rounds
+// the exact product once, where the reference rounds to f32 first).
+__device__ __forceinline__ float materialize(float v) {
+    __asm__ volatile("" : "+v"(v));
+    return v;
+}
+
+__device__ __forceinline__ uint16_t f2h(float v) {  // IEEE RNE of the f32 value
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(materialize(v)));
 }
 
 }  // namespace atlas

@@ -83,13 +83,19 @@ __device__ __forceinline__ void stage_row(uint8_t* dst, const uint8_t* src, uint
     }
 }
 
-// FP32 gather: one wave per token, 4 tokens per block.
-__global__ __launch_bounds__(256) void embed_f32_kernel(const float* table, const uint32_t* ids, float* out,
-                                                        uint32_t vocab, uint32_t hidden, uint32_t tokens,
-                                                        float scale, int vec) {
-    const uint32_t lane = threadIdx.x & (kWave - 1);
-    const uint32_t t = blockIdx.x * 4 + threadIdx.x / kWave;
-    if (t >= tokens) return;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void stg_nt(float* p, f32x4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+}
+
+// FP32 gather: one wavefront per token; the id is wave-uniform (scalar load).
+__global__ __launch_bounds__(64) void embed_f32_kernel(const float* __restrict__ table,
+                                                       const uint32_t* __restrict__ ids,
+                                                       float* __restrict__ out, uint32_t vocab,
+                                                       uint32_t hidden, float scale, int vec) {
+    const uint32_t lane = threadIdx.x;
+    const uint32_t t = blockIdx.x;
     const uint32_t id = ids[t];
     float* dst = out + static_cast<size_t>(t) * hidden;
     const bool valid = id < vocab;
@@ -97,9 +103,9 @@ __global__ __launch_bounds__(256) void embed_f32_kernel(const float* table, cons
     const bool scaled = scale != 1.0f;
     if (vec) {
         for (uint32_t c = lane * 4; c < hidden; c += 4 * kWave) {
-            float4 v = valid ? *reinterpret_cast<const float4*>(src + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-            if (scaled) v = make_float4(v.x * scale, v.y * scale, v.z * scale, v.w * scale);
-            *reinterpret_cast<float4*>(dst + c) = v;
+            f32x4 v = valid ? *reinterpret_cast<const f32x4*>(src + c) : f32x4{0.f, 0.f, 0.f, 0.f};
+            if (scaled) v = f32x4{v.x * scale, v.y * scale, v.z * scale, v.w * scale};
+            stg_nt(dst + c, v);
         }
     } else {
         for (uint32_t c = lane; c < hidden; c += kWave) {
@@ -109,24 +115,24 @@ __global__ __launch_bounds__(256) void embed_f32_kernel(const float* table, cons
     }
 }
 
-// Q4_0 / Q6_K gather: one wave per token, 4 tokens per block, packed rows in LDS.
+// Q4_0 / Q6_K gather: one wavefront per token.  The packed row is pulled into
+// LDS with the widest coalesced load its alignment allows, then each lane
+// decodes four consecutive values per step and writes them with one 128-bit
+// nontemporal store.
 template <bool Q6>
-__global__ __launch_bounds__(256) void embed_quant_kernel(const uint8_t* table, const uint32_t* ids, float* out,
-                                                          uint32_t vocab, uint32_t hidden, uint32_t tokens,
-                                                          float scale) {
-    extern __shared__ uint8_t lds[];
-    const uint32_t lane = threadIdx.x & (kWave - 1);
-    const uint32_t wave = threadIdx.x / kWave;
-    const uint32_t t = blockIdx.x * 4 + wave;
-    const uint32_t id = t < tokens ? ids[t] : vocab;
+__global__ __launch_bounds__(64) void embed_quant_kernel(const uint8_t* __restrict__ table,
+                                                         const uint32_t* __restrict__ ids,
+                                                         float* __restrict__ out, uint32_t vocab,
+                                                         uint32_t hidden, float scale) {
+    extern __shared__ uint8_t row[];
+    const uint32_t lane = threadIdx.x;
+    const uint32_t t = blockIdx.x;
+    const uint32_t id = ids[t];
     // the reference kernels leave rows with id >= vocab untouched
-    const bool active = id < vocab;
+    if (id >= vocab) return;
     const uint32_t row_bytes = Q6 ? (hidden / 256) * 210 : (hidden / 32) * 18;
-    const uint32_t pitch = (row_bytes + 15) & ~15u;
-    uint8_t* row = lds + wave * pitch;
-    if (active) stage_row(row, table + static_cast<size_t>(id) * row_bytes, row_bytes, lane, kWave);
-    __syncthreads();  // every wave of the block reaches this barrier
-    if (!active) return;
+    stage_row(row, table + static_cast<size_t>(id) * row_bytes, row_bytes, lane, kWave);
+    __syncthreads();
     float* dst = out + static_cast<size_t>(t) * hidden;
     for (uint32_t c = lane * 4; c < hidden; c += 4 * kWave) {
         float v[4];
@@ -134,40 +140,73 @@ __global__ __launch_bounds__(256) void embed_quant_kernel(const uint8_t* table, 
             q6_k_decode4(row, c, v);
         else
             q4_0_decode4(row, c, v);
-        *reinterpret_cast<float4*>(dst + c) = make_float4(v[0] * scale, v[1] * scale, v[2] * scale, v[3] * scale);
+        stg_nt(dst + c, f32x4{v[0] * scale, v[1] * scale, v[2] * scale, v[3] * scale});
     }
 }
 
 // PLE: one 256-thread block per token.
 //   out[t, j] = ((deq(table[id])[j] * embedding_scale) + projection[t, j]) * output_scale
-template <bool Q6>
-__global__ __launch_bounds__(256) void ple_quant_kernel(const uint8_t* table, const uint32_t* ids,
-                                                        const float* projection, float* out, uint32_t vocab,
-                                                        uint32_t row_elems, uint32_t tokens,
-                                                        float embedding_scale, float output_scale) {
+// The projection row (the dominant stream) is requested before the table row
+// is staged, IT float4 per thread, so its latency overlaps the gather.
+template <bool Q6, int IT>
+__global__ __launch_bounds__(256) void ple_quant_kernel(const uint8_t* __restrict__ table,
+                                                        const uint32_t* __restrict__ ids,
+                                                        const float* __restrict__ projection,
+                                                        float* __restrict__ out, uint32_t vocab,
+                                                        uint32_t row_elems, float embedding_scale,
+                                                        float output_scale) {
     extern __shared__ uint8_t row[];
     const uint32_t t = blockIdx.x;
-    if (t >= tokens) return;
     const uint32_t id = ids[t];
     if (id >= vocab) return;
+    const uint32_t n4 = row_elems / 4;
+    const size_t base = static_cast<size_t>(t) * row_elems;
+    f32x4 p[IT];
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+        const uint32_t c4 = min(threadIdx.x + 256u * i, n4 - 1);
+        p[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(projection + base) + c4);
+    }
     const uint32_t row_bytes = Q6 ? (row_elems / 256) * 210 : (row_elems / 32) * 18;
     stage_row(row, table + static_cast<size_t>(id) * row_bytes, row_bytes, threadIdx.x, blockDim.x);
     __syncthreads();
-    const size_t base = static_cast<size_t>(t) * row_elems;
-    for (uint32_t c = threadIdx.x * 4; c < row_elems; c += 4 * blockDim.x) {
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+        const uint32_t c4 = threadIdx.x + 256u * i;
+        if (c4 >= n4) break;
         float v[4];
         if (Q6)
-            q6_k_decode4(row, c, v);
+            q6_k_decode4(row, 4 * c4, v);
         else
-            q4_0_decode4(row, c, v);
-        const float4 p = *reinterpret_cast<const float4*>(projection + base + c);
-        float4 r;
-        r.x = (v[0] * embedding_scale + p.x) * output_scale;
-        r.y = (v[1] * embedding_scale + p.y) * output_scale;
-        r.z = (v[2] * embedding_scale + p.z) * output_scale;
-        r.w = (v[3] * embedding_scale + p.w) * output_scale;
-        *reinterpret_cast<float4*>(out + base + c) = r;
+            q4_0_decode4(row, 4 * c4, v);
+        const f32x4 q = p[i];
+        stg_nt(out + base + 4 * c4, f32x4{(v[0] * embedding_scale + q.x) * output_scale,
+                                          (v[1] * embedding_scale + q.y) * output_scale,
+                                          (v[2] * embedding_scale + q.z) * output_scale,
+                                          (v[3] * embedding_scale + q.w) * output_scale});
     }
+}
+
+template <bool Q6>
+hipError_t launch_ple_it(hipStream_t stream, const uint8_t* table, const uint32_t* ids, const float* projection,
+                         float* out, uint32_t vocab, uint32_t row_elems, uint32_t tokens, float es, float os) {
+    const uint32_t row_bytes = Q6 ? (row_elems / 256) * 210 : (row_elems / 32) * 18;
+    const size_t lds = (row_bytes + 15) & ~15u;
+    const uint32_t it = (row_elems / 4 + 255) / 256;
+#define ATLAS_PLE_CASE(N)                                                                                    \
+    case N:                                                                                                  \
+        hipLaunchKernelGGL((ple_quant_kernel<Q6, N>), dim3(tokens), dim3(256), lds, stream, table, ids,     \
+                           projection, out, vocab, row_elems, es, os);                                       \
+        break;
+    switch (it) {
+        ATLAS_PLE_CASE(1) ATLAS_PLE_CASE(2) ATLAS_PLE_CASE(3) ATLAS_PLE_CASE(4) ATLAS_PLE_CASE(5)
+        ATLAS_PLE_CASE(6) ATLAS_PLE_CASE(7) ATLAS_PLE_CASE(8) ATLAS_PLE_CASE(9) ATLAS_PLE_CASE(10)
+        ATLAS_PLE_CASE(11) ATLAS_PLE_CASE(12) ATLAS_PLE_CASE(13) ATLAS_PLE_CASE(14) ATLAS_PLE_CASE(15)
+        ATLAS_PLE_CASE(16)
+        default: return hipErrorInvalidValue;
+    }
+#undef ATLAS_PLE_CASE
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -176,22 +215,21 @@ hipError_t launch_embed_f32(hipStream_t stream, const float* table, const uint32
                             uint32_t vocab, uint32_t hidden, uint32_t tokens, float scale) {
     const int vec = (hidden % 4) == 0 && (reinterpret_cast<uintptr_t>(table) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(out) & 15) == 0;
-    hipLaunchKernelGGL(embed_f32_kernel, dim3((tokens + 3) / 4), dim3(256), 0, stream, table, ids, out, vocab,
-                       hidden, tokens, scale, vec);
+    hipLaunchKernelGGL(embed_f32_kernel, dim3(tokens), dim3(kWave), 0, stream, table, ids, out, vocab, hidden,
+                       scale, vec);
     return hipGetLastError();
 }
 
 hipError_t launch_embed_quant(hipStream_t stream, int q6k, const uint8_t* table, const uint32_t* ids,
                               float* out, uint32_t vocab, uint32_t hidden, uint32_t tokens, float scale) {
     const uint32_t row_bytes = q6k ? (hidden / 256) * 210 : (hidden / 32) * 18;
-    const size_t lds = 4 * static_cast<size_t>((row_bytes + 15) & ~15u);
-    const dim3 grid((tokens + 3) / 4);
+    const size_t lds = (row_bytes + 15) & ~15u;
     if (q6k)
-        hipLaunchKernelGGL((embed_quant_kernel<true>), grid, dim3(256), lds, stream, table, ids, out, vocab,
-                           hidden, tokens, scale);
+        hipLaunchKernelGGL((embed_quant_kernel<true>), dim3(tokens), dim3(kWave), lds, stream, table, ids, out,
+                           vocab, hidden, scale);
     else
-        hipLaunchKernelGGL((embed_quant_kernel<false>), grid, dim3(256), lds, stream, table, ids, out, vocab,
-                           hidden, tokens, scale);
+        hipLaunchKernelGGL((embed_quant_kernel<false>), dim3(tokens), dim3(kWave), lds, stream, table, ids, out,
+                           vocab, hidden, scale);
     return hipGetLastError();
 }
 
@@ -199,15 +237,11 @@ hipError_t launch_ple_quant(hipStream_t stream, int q6k, const uint8_t* table, c
                             const float* projection, float* out, uint32_t vocab, uint32_t layers,
                             uint32_t width, uint32_t tokens, float embedding_scale, float output_scale) {
     const uint32_t row_elems = layers * width;
-    const uint32_t row_bytes = q6k ? (row_elems / 256) * 210 : (row_elems / 32) * 18;
-    const size_t lds = (row_bytes + 15) & ~15u;
     if (q6k)
-        hipLaunchKernelGGL((ple_quant_kernel<true>), dim3(tokens), dim3(256), lds, stream, table, ids, projection,
-                           out, vocab, row_elems, tokens, embedding_scale, output_scale);
-    else
-        hipLaunchKernelGGL((ple_quant_kernel<false>), dim3(tokens), dim3(256), lds, stream, table, ids, projection,
-                           out, vocab, row_elems, tokens, embedding_scale, output_scale);
-    return hipGetLastError();
+        return launch_ple_it<true>(stream, table, ids, projection, out, vocab, row_elems, tokens, embedding_scale,
+                                   output_scale);
+    return launch_ple_it<false>(stream, table, ids, projection, out, vocab, row_elems, tokens, embedding_scale,
+                                output_scale);
 }
 
 }  // namespace atlas

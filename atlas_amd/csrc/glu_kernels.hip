@@ -30,20 +30,24 @@ __device__ __forceinline__ float elt(float a, float b, float scalar) {
 
 constexpr bool binary(int op) { return op == kEltSwiglu || op == kEltGeglu || op == kEltAdd || op == kEltMul; }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// One float4 per operand per thread per iteration, nontemporal loads and
+// stores (each byte is touched once, so caching it only evicts other data).
 template <int OP>
 __global__ __launch_bounds__(256) void elementwise_vec_kernel(const float* a, const float* b,
                                                               float scalar, float* out, uint64_t n4) {
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
-        float4 va = reinterpret_cast<const float4*>(a)[i];
-        float4 vb = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (binary(OP)) vb = reinterpret_cast<const float4*>(b)[i];
-        float4 r;
+        const f32x4 va = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a) + i);
+        f32x4 vb = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (binary(OP)) vb = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(b) + i);
+        f32x4 r;
         r.x = elt<OP>(va.x, vb.x, scalar);
         r.y = elt<OP>(va.y, vb.y, scalar);
         r.z = elt<OP>(va.z, vb.z, scalar);
         r.w = elt<OP>(va.w, vb.w, scalar);
-        reinterpret_cast<float4*>(out)[i] = r;
+        __builtin_nontemporal_store(r, reinterpret_cast<f32x4*>(out) + i);
     }
 }
 
@@ -56,20 +60,24 @@ __global__ __launch_bounds__(256) void elementwise_scalar_kernel(const float* a,
         out[i] = elt<OP>(a[i], binary(OP) ? b[i] : 0.0f, scalar);
 }
 
-struct h4 {
-    uint16_t v[4];
-};
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Eight f16 values per operand per thread (one 128-bit nontemporal access).
+__device__ __forceinline__ uint32_t swiglu_f16_pair(uint32_t g, uint32_t u) {
+    const uint32_t lo = f2h(silu_f32(h2f(static_cast<uint16_t>(g))) * h2f(static_cast<uint16_t>(u)));
+    const uint32_t hi = f2h(silu_f32(h2f(static_cast<uint16_t>(g >> 16))) * h2f(static_cast<uint16_t>(u >> 16)));
+    return lo | (hi << 16);
+}
 
 __global__ __launch_bounds__(256) void swiglu_f16_kernel(const uint16_t* gate, const uint16_t* up,
-                                                         uint16_t* out, uint64_t n4) {
+                                                         uint16_t* out, uint64_t n8) {
     const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
-    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride) {
-        h4 g = reinterpret_cast<const h4*>(gate)[i];
-        h4 u = reinterpret_cast<const h4*>(up)[i];
-        h4 r;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) r.v[j] = f2h(silu_f32(h2f(g.v[j])) * h2f(u.v[j]));
-        reinterpret_cast<h4*>(out)[i] = r;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n8; i += stride) {
+        const u32x4 g = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gate) + i);
+        const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(up) + i);
+        const u32x4 r{swiglu_f16_pair(g.x, u.x), swiglu_f16_pair(g.y, u.y), swiglu_f16_pair(g.z, u.z),
+                      swiglu_f16_pair(g.w, u.w)};
+        __builtin_nontemporal_store(r, reinterpret_cast<u32x4*>(out) + i);
     }
 }
 
@@ -94,11 +102,12 @@ __global__ __launch_bounds__(256) void geglu_offset_kernel(const float* gate, co
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// 256-thread blocks; at most 8 blocks per CU worth of grid (256 CUs), the
-// rest is covered by the grid-stride loop.
+// 256-thread blocks, one work item per thread up to 2^20 blocks (one pass
+// over the data measured fastest on MI355X); larger ranges use the
+// grid-stride loop.
 uint32_t grid_for(uint64_t work_items) {
     uint64_t blocks = (work_items + 255) / 256;
-    const uint64_t cap = 256ull * 16;
+    const uint64_t cap = 1ull << 20;
     if (blocks > cap) blocks = cap;
     if (blocks == 0) blocks = 1;
     return static_cast<uint32_t>(blocks);
@@ -138,13 +147,12 @@ hipError_t launch_elementwise_f32(hipStream_t stream, EltOp op, const float* a, 
 
 hipError_t launch_swiglu_f16(hipStream_t stream, const uint16_t* gate, const uint16_t* up, uint16_t* out,
                              uint64_t n) {
-    const bool vec = (reinterpret_cast<uintptr_t>(gate) & 7) == 0 &&
-                     (reinterpret_cast<uintptr_t>(up) & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 7) == 0;
+    const bool vec = aligned16(gate) && aligned16(up) && aligned16(out);
     uint64_t done = 0;
-    if (vec && n >= 4) {
-        const uint64_t n4 = n / 4;
-        hipLaunchKernelGGL(swiglu_f16_kernel, dim3(grid_for(n4)), dim3(256), 0, stream, gate, up, out, n4);
-        done = n4 * 4;
+    if (vec && n >= 8) {
+        const uint64_t n8 = n / 8;
+        hipLaunchKernelGGL(swiglu_f16_kernel, dim3(grid_for(n8)), dim3(256), 0, stream, gate, up, out, n8);
+        done = n8 * 8;
     }
     if (done < n) {
         const uint64_t rest = n - done;

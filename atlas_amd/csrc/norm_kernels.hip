@@ -204,10 +204,187 @@ __global__ __launch_bounds__(256) void rms_wide_kernel(NormArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Register engine: sequential order, the default for 16-byte-aligned rows of
+// at most 2048 floats.  One wavefront owns R rows.  Lane l keeps float4
+// column c = l + 64*j (j < J) of each of its rows in registers, so HBM sees
+// every input once and every output once:
+//   1. every load of the wave is issued up front (the rows, the epilogue
+//      operand -- residual or state -- and the weights), streamed with
+//      nontemporal loads;
+//   2. as chunk j lands, its squares go to LDS and lane r folds row r's
+//      chunk j in index order while later chunks are still in flight.  The
+//      f32 fold is a dependent add chain (~8 cycles per add on gfx950, ~12K
+//      cycles for 1536 values), so it must overlap the loads rather than sit
+//      between the load and store phases;
+//   3. lane r's inverse RMS is broadcast with readlane and every lane
+//      finishes its columns with nontemporal stores.
+// Each row is fully read before any of its outputs is written, so the
+// aliased bindings of the reference call sites stay valid.
+// ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 ldg_nt(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+}
+__device__ __forceinline__ f32x4 ldg(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ void stg_nt(float* p, f32x4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+}
+
+template <int R, int J, int MODE>
+__global__ __launch_bounds__(64) void rms_reg_kernel(NormArgs a) {
+    // Squares of R rows, (hidden/4 + 1) float4 per row.  The load phase is
+    // straight-line code (rows past the end and columns past the row width
+    // are clamped to valid duplicate addresses and never stored), so the
+    // compiler can wait for chunk j's loads alone before folding it.
+    extern __shared__ f32x4 sq4[];
+    constexpr bool kOperand = MODE != kNormPlain;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t h = a.hidden;
+    const uint32_t nv = h >> 2;
+    const uint32_t stride4 = nv + 1;
+    const uint32_t row0 = blockIdx.x * R;
+    const uint32_t nrows = min(static_cast<uint32_t>(R), a.rows - row0);
+    // second operand: residual (kNormResidual, kNormAddNorm) or state (kNormAddScale)
+    const float* operand = MODE == kNormAddScale ? a.out : a.residual;
+
+    f32x4 x[R][J];
+    f32x4 e[kOperand ? R : 1][kOperand ? J : 1];
+    f32x4 w[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t c = min(lane + 64u * j, nv - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const size_t idx = static_cast<size_t>(row0 + min(static_cast<uint32_t>(r), nrows - 1)) * h + 4 * c;
+            x[r][j] = ldg_nt(a.x + idx);
+            if (kOperand) e[r][j] = ldg_nt(operand + idx);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) w[j] = ldg(a.weight + 4 * min(lane + 64u * j, nv - 1));
+
+    float s = 0.0f;  // lane r < nrows: running sum of squares of row r
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t creal = lane + 64u * j;
+        const uint32_t c = min(creal, nv - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            f32x4 v = x[r][j];
+            if (MODE == kNormAddNorm) {
+                const f32x4 b = e[r][j];
+                v = f32x4{v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w};
+                x[r][j] = v;
+            }
+            sq4[r * stride4 + c] = f32x4{v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w};
+        }
+        __syncthreads();
+        if (lane < nrows) {
+            const uint32_t end = min(nv, 64u * (j + 1));
+            const f32x4* row = sq4 + lane * stride4;
+#pragma unroll 8
+            for (uint32_t k = 64u * j; k < end; ++k) {
+                const f32x4 v = row[k];
+                s = s + v.x;
+                s = s + v.y;
+                s = s + v.z;
+                s = s + v.w;
+            }
+        }
+    }
+    if (MODE == kNormAddNorm) {  // stored residual stream r = x + residual
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (static_cast<uint32_t>(r) >= nrows) break;
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const uint32_t c = lane + 64u * j;
+                if (c < nv) stg_nt(a.residual_out + static_cast<size_t>(row0 + r) * h + 4 * c, x[r][j]);
+            }
+        }
+    }
+
+    const float inv = lane < nrows ? inverse_rms(s, static_cast<float>(h), a.epsilon) : 0.0f;
+    const float scale = MODE == kNormAddScale ? *a.scale : 1.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (static_cast<uint32_t>(r) >= nrows) break;
+        const float ir = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t c = lane + 64u * j;
+            if (c >= nv) continue;
+            const size_t idx = static_cast<size_t>(row0 + r) * h + 4 * c;
+            const f32x4 v = x[r][j], ww = w[j];
+            const f32x4 n{v.x * ir * ww.x, v.y * ir * ww.y, v.z * ir * ww.z, v.w * ir * ww.w};
+            if (MODE == kNormPlain || MODE == kNormAddNorm) {
+                stg_nt(a.out + idx, n);
+            } else if (MODE == kNormResidual) {
+                if (a.normalized) stg_nt(a.normalized + idx, n);
+                const f32x4 b = e[r][j];
+                stg_nt(a.out + idx, f32x4{b.x + n.x, b.y + n.y, b.z + n.z, b.w + n.w});
+            } else {
+                const f32x4 b = e[r][j];
+                stg_nt(a.out + idx,
+                       f32x4{(b.x + n.x) * scale, (b.y + n.y) * scale, (b.z + n.z) * scale, (b.w + n.w) * scale});
+            }
+        }
+    }
+}
+
 int env_int(const char* name, int fallback) {
     const char* v = getenv(name);
     if (!v || !*v) return fallback;
     return atoi(v);
+}
+
+bool lds_engine_forced() {
+    static const bool forced = env_int("ATLAS_NORM_LDS_ENGINE", 0) != 0;
+    return forced;
+}
+
+// Rows per wavefront for the register engine.
+int pick_reg_rows(uint32_t rows, int J, int mode) {
+    static const int forced = env_int("ATLAS_REG_ROWS", 0);
+    if (forced == 1 || forced == 2 || forced == 4) return forced;
+    // Measured on MI355X at [4096, 1536]: R = 2 (two wavefronts per SIMD)
+    // beats R = 4 (one wavefront per SIMD) by 20-30 % and R = 1 by 10-35 %.
+    (void)J;
+    (void)mode;
+    return rows >= 2048 ? 2 : 1;
+}
+
+template <int R, int J, int MODE>
+hipError_t launch_reg_rj(hipStream_t s, const NormArgs& a) {
+    const size_t lds = static_cast<size_t>(R) * (a.hidden / 4 + 1) * sizeof(f32x4);
+    hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE>), dim3((a.rows + R - 1) / R), dim3(kWave), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int R, int MODE>
+hipError_t launch_reg_r(hipStream_t s, const NormArgs& a, int J) {
+    switch (J) {
+        case 1: return launch_reg_rj<R, 1, MODE>(s, a);
+        case 2: return launch_reg_rj<R, 2, MODE>(s, a);
+        case 3: return launch_reg_rj<R, 3, MODE>(s, a);
+        case 4: return launch_reg_rj<R, 4, MODE>(s, a);
+        case 5: return launch_reg_rj<R, 5, MODE>(s, a);
+        case 6: return launch_reg_rj<R, 6, MODE>(s, a);
+        case 7: return launch_reg_rj<R, 7, MODE>(s, a);
+        default: return launch_reg_rj<R, 8, MODE>(s, a);
+    }
+}
+
+template <int MODE>
+hipError_t launch_reg(hipStream_t s, const NormArgs& a) {
+    const int J = static_cast<int>((a.hidden / 4 + 63) / 64);
+    switch (pick_reg_rows(a.rows, J, MODE)) {
+        case 4: return launch_reg_r<4, MODE>(s, a, J);
+        case 2: return launch_reg_r<2, MODE>(s, a, J);
+        default: return launch_reg_r<1, MODE>(s, a, J);
+    }
 }
 
 // Rows per wavefront for the sequential engine: enough wavefronts to keep
@@ -404,6 +581,13 @@ hipError_t launch_rms_norm_f32(hipStream_t stream, NormMode mode, Reduction red,
             case kNormResidual: return launch_wide<kNormResidual>(stream, a, vec);
             case kNormAddNorm: return launch_wide<kNormAddNorm>(stream, a, vec);
             case kNormAddScale: return launch_wide<kNormAddScale>(stream, a, vec);
+        }
+    } else if (vec && a.hidden <= 2048 && !lds_engine_forced()) {
+        switch (mode) {
+            case kNormPlain: return launch_reg<kNormPlain>(stream, a);
+            case kNormResidual: return launch_reg<kNormResidual>(stream, a);
+            case kNormAddNorm: return launch_reg<kNormAddNorm>(stream, a);
+            case kNormAddScale: return launch_reg<kNormAddScale>(stream, a);
         }
     } else {
         switch (mode) {

@@ -137,6 +137,10 @@ class HipRuntime:
     def memset(self, buf: DeviceBuffer, value: int, nbytes: int) -> None:
         self._check(self.lib.atlas_hip_memset(self.ctx, _ptr(buf), value, nbytes))
 
+    def copy(self, dst: DeviceBuffer, src: DeviceBuffer, nbytes: int) -> None:
+        """Device-to-device copy on the context stream."""
+        self._check(self.lib.atlas_hip_copy_d2d(self.ctx, _ptr(dst), _ptr(src), nbytes))
+
     def sync(self) -> None:
         self._check(self.lib.atlas_hip_sync(self.ctx))
 

@@ -13,17 +13,22 @@ synthetic, HBM-resident inputs:
     geglu        gelu_tanh(gate) * up                         [4096 x 6144]
 
 `value` = tokens / s for the whole step (T / wall time per step, inputs
-already resident).  Per-op achieved GB/s uses algorithmic bytes (each input
-read once, each output written once) over the op's average launch duration
-from HIP events around back-to-back launches that rotate over >= 4 buffer
-sets (> 1 GB in aggregate, so the 256 MB MALL cannot serve repeats).  The
-CPU baseline is the oracle (a single-threaded C restatement of the reference
-CPU operators) timed on this host over a bounded token sample.
+already resident in HBM).  Per-op achieved GB/s = algorithmic bytes (each
+input read once, each output written once) / the op's average launch
+duration, from HIP events on the library's stream around back-to-back
+launches.  Every op rotates over its own buffer sets -- table copies
+included -- totalling >= 1 GiB, so the 256 MB MALL cannot serve repeats.
+The CPU baseline is the oracle (a single-threaded C restatement of the
+reference CPU operators) timed on this host over a bounded token sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--reduction sequential|wide]
+       python bench.py --only geglu,rms_norm        (per-op timing only, for profiling)
+       python bench.py --only geglu --copy-mib 512  (plus a D2D copy of known size,
+                                                      the PMC calibration kernel)
 """
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -35,90 +40,106 @@ sys.path.insert(0, ROOT)
 
 METRIC = "achieved HBM GB/s (% of peak) per fused op; fused-op tokens/s at T=4096, 1 GPU"
 HBM_PEAK_GBS = 8000.0
+ROTATION_BYTES = 1 << 30
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def build_sets(rt, wl, nsets):
-    """Device buffers: shared tables + `nsets` rotating activation sets."""
-    L, Q = wl.GemmaLayerShape(), wl.QuantGatherShape()
-    T, H, D, QH, F = L.tokens, L.hidden, L.head_dim, L.q_heads, L.ffn
-    r = wl.rng(2024)
-    log("generating tables")
-    tables = {
-        "q4": rt.upload(wl.q4_0_table(r, Q.vocab, Q.hidden)),
-        "q6": rt.upload(wl.q6_k_table(r, Q.vocab, Q.hidden)),
-        "ple": rt.upload(wl.q4_0_table(r, Q.vocab, Q.ple_layers * Q.ple_width)),
-        "w": rt.upload(wl.normal(r, H, 1.0, 0.1)),
-        "qw": rt.upload(wl.normal(r, D, 1.0, 0.1)),
-        "kw": rt.upload(wl.normal(r, D, 1.0, 0.1)),
-    }
-    from atlas_amd import rope_tables_gemma4
+class Ops:
+    """The step's ops: host inputs, algorithmic bytes and launchers."""
 
-    cos, sin = rope_tables_gemma4(np.arange(T, dtype=np.uint32), D // 2, D, L.theta_local)
-    log("generating activations")
-    host = {
-        "x": wl.normal(r, T * H), "res": wl.normal(r, T * H),
-        "q": wl.normal(r, T * QH * D), "k": wl.normal(r, T * D), "cos": cos, "sin": sin,
-        "gate": wl.normal(r, T * F), "up": wl.normal(r, T * F),
-        "proj": wl.normal(r, T * Q.ple_layers * Q.ple_width),
-    }
-    outs = {"y": T * H, "out": T * H, "qo": T * QH * D, "ko": T * D, "glu": T * F, "e4": T * H, "e6": T * H,
-            "pleo": T * Q.ple_layers * Q.ple_width}
-    sets = []
-    for i in range(nsets):
-        s = {k: rt.upload(v) for k, v in host.items()}
-        s["ids"] = rt.upload(wl.token_ids(wl.rng(77 + i), T, Q.vocab))
-        for k, n in outs.items():
-            s[k] = rt.empty(n)
-        sets.append(s)
-    return tables, sets
+    def __init__(self, wl, rope_tables):
+        L, Q = wl.GemmaLayerShape(), wl.QuantGatherShape()
+        self.L, self.Q = L, Q
+        T, H, D, QH, F = L.tokens, L.hidden, L.head_dim, L.q_heads, L.ffn
+        ple_row = Q.ple_layers * Q.ple_width
+        r = wl.rng(2024)
+        log("generating inputs")
+        cos, sin = rope_tables(np.arange(T, dtype=np.uint32), D // 2, D, L.theta_local)
+        self.host = {
+            "q4": wl.q4_0_table(r, Q.vocab, Q.hidden), "q6": wl.q6_k_table(r, Q.vocab, Q.hidden),
+            "ple": wl.q4_0_table(r, Q.vocab, ple_row), "ids": wl.token_ids(r, T, Q.vocab),
+            "w": wl.normal(r, H, 1.0, 0.1), "qw": wl.normal(r, D, 1.0, 0.1), "kw": wl.normal(r, D, 1.0, 0.1),
+            "x": wl.normal(r, T * H), "res": wl.normal(r, T * H), "q": wl.normal(r, T * QH * D),
+            "k": wl.normal(r, T * D), "cos": cos, "sin": sin, "gate": wl.normal(r, T * F),
+            "up": wl.normal(r, T * F), "proj": wl.normal(r, T * ple_row),
+        }
+        scale = float(wl.f32_sqrt(H))
+        es, os_ = 16.0, float(wl.SQRT_2_RECIP)
+        f4 = 4
+        # name: (inputs copied per set, outputs per set (elements), algorithmic bytes, launch)
+        self.table = {
+            "embed_q4_0": (["q4", "ids"], {"e4": T * H}, T * wl.q_row_bytes(H, False) + T * 4 + T * H * f4,
+                           lambda rt, s: rt.embed_q4_0(s["q4"], s["ids"], s["e4"], Q.vocab, H, T, scale)),
+            "embed_q6_k": (["q6", "ids"], {"e6": T * H}, T * wl.q_row_bytes(H, True) + T * 4 + T * H * f4,
+                           lambda rt, s: rt.embed_q6_k(s["q6"], s["ids"], s["e6"], Q.vocab, H, T, scale)),
+            "ple_q4_0": (["ple", "ids", "proj"], {"pleo": T * ple_row},
+                         T * wl.q_row_bytes(ple_row, False) + T * 4 + 2 * T * ple_row * f4,
+                         lambda rt, s: rt.ple_q4_0(s["ple"], s["ids"], s["proj"], s["pleo"], Q.vocab, Q.ple_layers,
+                                                   Q.ple_width, T, es, os_)),
+            "rms_norm": (["x", "w"], {"y": T * H}, 2 * T * H * f4 + H * f4,
+                         lambda rt, s: rt.rms_norm(s["x"], s["w"], s["y"], T, H, L.eps)),
+            "qk_norm_rope": (["q", "k", "qw", "kw", "cos", "sin"], {"qo": T * QH * D, "ko": T * D},
+                             2 * T * (QH + 1) * D * f4 + 2 * T * (D // 2) * f4 + 2 * D * f4,
+                             lambda rt, s: rt.qk_norm_rope(s["q"], s["k"], s["qw"], s["kw"], s["cos"], s["sin"],
+                                                           s["qo"], s["ko"], T, QH, 1, D, D // 2, L.eps)),
+            "rms_residual": (["x", "w", "res"], {"out": T * H}, 3 * T * H * f4 + H * f4,
+                             lambda rt, s: rt.rms_norm_residual(s["x"], s["w"], s["res"], None, s["out"], T, H,
+                                                                L.eps)),
+            "geglu": (["gate", "up"], {"glu": T * F}, 3 * T * F * f4,
+                      lambda rt, s: rt.geglu(s["gate"], s["up"], s["glu"], T * F)),
+        }
+
+    def set_bytes(self, name):
+        ins, outs, _, _ = self.table[name]
+        return sum(self.host[k].nbytes for k in ins) + sum(n * 4 for n in outs.values())
+
+    def build_sets(self, rt, names, nsets):
+        """`nsets` buffer sets holding every input/output of `names`.  Set 0 is
+        uploaded; the others are device-to-device copies at distinct addresses."""
+        keys = sorted({k for n in names for k in self.table[n][0]})
+        outs = {}
+        for n in names:
+            outs.update(self.table[n][1])
+        master = {k: rt.upload(self.host[k]) for k in keys}
+        sets = [master]
+        for _ in range(1, nsets):
+            s = {}
+            for k in keys:
+                b = rt.alloc(master[k].nbytes, master[k].dtype)
+                rt.copy(b, master[k], master[k].nbytes)
+                s[k] = b
+            sets.append(s)
+        for s in sets:
+            for k, n in outs.items():
+                s[k] = rt.empty(n)
+        rt.sync()
+        return sets
+
+    def free_sets(self, rt, sets):
+        for s in sets:
+            for b in s.values():
+                rt.free(b)
 
 
-def op_table(wl):
-    L, Q = wl.GemmaLayerShape(), wl.QuantGatherShape()
-    T, H, D, QH, F = L.tokens, L.hidden, L.head_dim, L.q_heads, L.ffn
-    ple_row = Q.ple_layers * Q.ple_width
-    scale = float(wl.f32_sqrt(H))
-    es, os_ = 16.0, float(wl.SQRT_2_RECIP)
-    return {
-        # name: (algorithmic bytes per launch, launch(rt, tables, set))
-        "embed_q4_0": (T * wl.q_row_bytes(H, False) + T * 4 + T * H * 4,
-                       lambda rt, t, s: rt.embed_q4_0(t["q4"], s["ids"], s["e4"], Q.vocab, H, T, scale)),
-        "embed_q6_k": (T * wl.q_row_bytes(H, True) + T * 4 + T * H * 4,
-                       lambda rt, t, s: rt.embed_q6_k(t["q6"], s["ids"], s["e6"], Q.vocab, H, T, scale)),
-        "ple_q4_0": (T * wl.q_row_bytes(ple_row, False) + T * 4 + 2 * T * ple_row * 4,
-                     lambda rt, t, s: rt.ple_q4_0(t["ple"], s["ids"], s["proj"], s["pleo"], Q.vocab, Q.ple_layers,
-                                                  Q.ple_width, T, es, os_)),
-        "rms_norm": (2 * T * H * 4 + H * 4,
-                     lambda rt, t, s: rt.rms_norm(s["x"], t["w"], s["y"], T, H, L.eps)),
-        "qk_norm_rope": (2 * T * (QH + 1) * D * 4 + 2 * T * (D // 2) * 4 + 2 * D * 4,
-                         lambda rt, t, s: rt.qk_norm_rope(s["q"], s["k"], t["qw"], t["kw"], s["cos"], s["sin"],
-                                                          s["qo"], s["ko"], T, QH, 1, D, D // 2, L.eps)),
-        "rms_residual": (3 * T * H * 4 + H * 4,
-                         lambda rt, t, s: rt.rms_norm_residual(s["x"], t["w"], s["res"], None, s["out"], T, H,
-                                                               L.eps)),
-        "geglu": (3 * T * F * 4, lambda rt, t, s: rt.geglu(s["gate"], s["up"], s["glu"], T * F)),
-    }
-
-
-def time_op(rt, launch, tables, sets, iters):
+def time_launches(rt, launch, sets, iters):
     for i in range(3):
-        launch(rt, tables, sets[i % len(sets)])
+        launch(rt, sets[i % len(sets)])
     rt.sync()
     a, b = rt.event(), rt.event()
     rt.record(a)
     for i in range(iters):
-        launch(rt, tables, sets[i % len(sets)])
+        launch(rt, sets[i % len(sets)])
     rt.record(b)
     rt.sync()
     return rt.elapsed_ms(a, b) / iters
 
 
 def cpu_baseline(wl, budget_s=10.0):
-    """Single-threaded oracle over a token sample of the same step (TEST-ONLY oracle)."""
+    """Single-threaded oracle over a token sample of the same step (the oracle is
+    test infrastructure; here it is the reported CPU baseline, never the product)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as ora
 
@@ -126,7 +147,7 @@ def cpu_baseline(wl, budget_s=10.0):
     Ts, H, D, QH, F = 64, L.hidden, L.head_dim, L.q_heads, L.ffn
     ple_row = Q.ple_layers * Q.ple_width
     r = wl.rng(99)
-    vocab = 4096  # gather cost does not depend on the vocabulary size
+    vocab = 4096  # a gather's cost does not depend on the vocabulary size
     q4, q6, pt = wl.q4_0_table(r, vocab, H), wl.q6_k_table(r, vocab, H), wl.q4_0_table(r, vocab, ple_row)
     ids = wl.token_ids(r, Ts, vocab)
     x, res, w = wl.normal(r, Ts * H), wl.normal(r, Ts * H), wl.normal(r, H, 1, 0.1)
@@ -152,7 +173,19 @@ def cpu_baseline(wl, budget_s=10.0):
     el = time.perf_counter() - t0
     return {"value": round(Ts * reps / el, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
             "sample": f"{reps} passes of the full step over {Ts} tokens ({el:.1f} s), single-threaded C oracle "
-                      f"(-O2, -ffp-contract=off), same op list and shapes per token"}
+                      f"(-O2, -ffp-contract=off), same op list and per-token shapes (gather vocab 4096)"}
+
+
+def pmc_traffic(kernel_op):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, or None."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = data.get("ops", {}).get(kernel_op)
+    return None if entry is None else entry.get("traffic_bytes")
 
 
 def main():
@@ -160,47 +193,66 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--sets", type=int, default=4)
     ap.add_argument("--op-iters", type=int, default=100)
+    ap.add_argument("--step-sets", type=int, default=4)
     ap.add_argument("--reduction", choices=["sequential", "wide"], default="sequential")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma-separated op subset for per-op timing (profiling)")
+    ap.add_argument("--only", default="", help="comma-separated op subset: per-op timing only (profiling)")
+    ap.add_argument("--copy-mib", type=int, default=0, help="also time a device-to-device copy of this size")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: every op of this path is row-independent and no multi-GPU "
-              "figure is produced (see DESIGN.md for how tokens would shard). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU only: every op of this path is row-independent and this build "
+              "produces no multi-GPU figure (DESIGN.md describes how tokens would shard). Run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
 
-    from atlas_amd import ATLAS_REDUCTION_SEQUENTIAL, ATLAS_REDUCTION_WIDE, HipRuntime
+    from atlas_amd import ATLAS_REDUCTION_SEQUENTIAL, ATLAS_REDUCTION_WIDE, HipRuntime, rope_tables_gemma4
     from atlas_amd import workloads as wl
 
     rt = HipRuntime(0, ATLAS_REDUCTION_WIDE if args.reduction == "wide" else ATLAS_REDUCTION_SEQUENTIAL)
-    tables, sets = build_sets(rt, wl, args.sets)
-    ops = op_table(wl)
-    L = wl.GemmaLayerShape()
-    T = L.tokens
+    ops = Ops(wl, rope_tables_gemma4)
+    T = ops.L.tokens
     only = [o for o in args.only.split(",") if o]
-
-    def step(i):
-        s = sets[i % len(sets)]
-        for _, (_, launch) in ops.items():
-            launch(rt, tables, s)
+    for o in only:
+        if o not in ops.table:
+            sys.exit(f"unknown op {o}; choose from {', '.join(ops.table)}")
 
     per_op = {}
-    for name, (nbytes, launch) in ops.items():
+    for name, (_, _, nbytes, launch) in ops.table.items():
         if only and name not in only:
             continue
-        log(f"timing {name}")
-        ms = time_op(rt, launch, tables, sets, args.op_iters)
+        nsets = max(4, math.ceil(ROTATION_BYTES / ops.set_bytes(name)))
+        log(f"timing {name} ({nsets} rotating sets)")
+        sets = ops.build_sets(rt, [name], nsets)
+        ms = time_launches(rt, launch, sets, args.op_iters)
+        ops.free_sets(rt, sets)
         gbs = nbytes / (ms * 1e-3) / 1e9
         per_op[name] = {"us": round(ms * 1e3, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
-                        "frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(T / (ms * 1e-3), 1)}
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+                        "rotating_sets": nsets}
+    if args.copy_mib:
+        n = args.copy_mib << 20
+        src, dst = rt.alloc(n), rt.alloc(n)
+        rt.memset(src, 1, n)
+        for _ in range(5):
+            rt.copy(dst, src, n)
+        rt.sync()
+        log(f"copied {args.copy_mib} MiB x5 (PMC calibration)")
     if only:
         print(json.dumps({"per_op": per_op}))
+        rt.close()
         return
 
     log("timed steps")
+    names = list(ops.table)
+    sets = ops.build_sets(rt, names, args.step_sets)
+
+    def step(i):
+        s = sets[i % len(sets)]
+        for nm in names:
+            ops.table[nm][3](rt, s)
+
     for i in range(args.warmup):
         step(i)
     rt.sync()
@@ -214,9 +266,9 @@ def main():
     wall = time.perf_counter() - t0
     ev_ms = rt.elapsed_ms(a, b)
     ms_per_step = wall * 1e3 / args.steps
-    step_bytes = sum(v[0] for v in ops.values())
+    step_bytes = sum(v[2] for v in ops.table.values())
 
-    dom = max(ops, key=lambda n: ops[n][0])
+    dom = max(per_op, key=lambda n: per_op[n]["us"])
     d = per_op[dom]
     result = {
         "metric": METRIC,
@@ -231,13 +283,14 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "gemma4-e2b-fused-ops-T4096 (C3 layer ops + C4 gathers, one pass of each op)",
-                   "tokens": T, "hidden": L.hidden, "q_heads": L.q_heads, "head_dim": L.head_dim, "ffn": L.ffn,
-                   "vocab": wl.QuantGatherShape().vocab, "ple": "35x256 Q4_0", "reduction": args.reduction,
-                   "buffer_sets": args.sets, "step_bytes": step_bytes,
+        "config": {"workload": "gemma4-e2b-fused-ops-T4096 (configs[2] layer ops + configs[3] gathers, "
+                               "one pass of each op per step)",
+                   "tokens": T, "hidden": ops.L.hidden, "q_heads": ops.L.q_heads, "head_dim": ops.L.head_dim,
+                   "ffn": ops.L.ffn, "vocab": ops.Q.vocab, "ple": "35x256 Q4_0", "reduction": args.reduction,
+                   "step_sets": args.step_sets, "step_bytes": step_bytes,
                    "step_GB/s": round(step_bytes / (ev_ms * 1e-3 / args.steps) / 1e9, 1)},
-        "roofline": {"kernel": dom, "bound": "hbm", "achieved": d["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": d["frac"], "traffic": None,
+        "roofline": {"bound": "hbm", "achieved": d["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": d["frac"], "traffic": pmc_traffic(dom), "kernel": dom,
                      "algorithmic_bytes_per_launch": d["bytes"], "avg_launch_us": d["us"]},
         "ops": per_op,
     }

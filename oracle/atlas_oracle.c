@@ -100,12 +100,13 @@ static float pow2i(int k) { /* 2^k for k in [-126, 127] */
 /* binary32 exp by Cody & Waite argument reduction (Cody and Waite, "Software
  * Manual for the Elementary Functions", 1980: x = n ln2 + r with ln2 split
  * into a 9-bit head and a tail so n*head is exact) and the degree-7 Taylor
- * polynomial of e^r on |r| <= ln2/2 (truncation < 2^-27 relative).  Only
- * IEEE add/sub/mul, floor and exponent-field assembly are used, so the same
- * steps give the same bits wherever they are compiled without contraction.
- * The reference evaluates Metal's exp (crates/atlas-metal/src/kernels.metal:
- * 27-36, 742-750); its bits are not pinned, so this oracle pins against
- * float64 exp (tests/test_oracle_math.py). */
+ * polynomial of e^r on |r| <= ln2/2 (truncation < 2^-27 relative) in Horner
+ * form with fused multiply-adds.  Only IEEE fma, floor and exact powers of
+ * two are used (C99 fmaf is a correctly rounded fused multiply-add), so the
+ * same steps give the same bits on the GPU.  The reference evaluates
+ * Metal's exp (crates/atlas-metal/src/kernels.metal:27-36, 742-750); its
+ * bits are not pinned, so this function is pinned against float64 exp
+ * (tests/test_oracle_pins.py: faithful, < 1 ulp). */
 float oracle_expf(float x) {
     if (x != x) return x;
     if (x > 89.0f) return INFINITY;
@@ -113,16 +114,17 @@ float oracle_expf(float x) {
     const float log2e = 1.44269502162933349609375f; /* nearest f32 to log2(e) */
     const float ln2_hi = 0.693359375f;              /* 355/512 */
     const float ln2_lo = -2.12194440e-4f;           /* ln2 - ln2_hi */
-    float fn = floorf(x * log2e + 0.5f);
+    float fn = floorf(fmaf(x, log2e, 0.5f));
     int n = (int)fn;
-    float r = (x - fn * ln2_hi) - fn * ln2_lo;
-    float poly = 1.0f / 5040.0f;
-    poly = 1.0f / 720.0f + r * poly;
-    poly = 1.0f / 120.0f + r * poly;
-    poly = 1.0f / 24.0f + r * poly;
-    poly = 1.0f / 6.0f + r * poly;
-    poly = 0.5f + r * poly;
-    float p = 1.0f + (r + (r * r) * poly);
+    float r = fmaf(-fn, ln2_lo, fmaf(-fn, ln2_hi, x));
+    float p = 1.0f / 5040.0f;
+    p = fmaf(p, r, 1.0f / 720.0f);
+    p = fmaf(p, r, 1.0f / 120.0f);
+    p = fmaf(p, r, 1.0f / 24.0f);
+    p = fmaf(p, r, 1.0f / 6.0f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
     if (n > 127) return (p * pow2i(127)) * pow2i(n - 127);
     if (n < -126) return (p * pow2i(n + 100)) * pow2i(-100);
     return p * pow2i(n);

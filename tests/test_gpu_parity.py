@@ -100,7 +100,8 @@ def test_golden_f16(rt, ora):
 
 # ------------------------------------------------- shapes, modes, edge cases
 
-@pytest.mark.parametrize("rows,hidden", [(1, 4), (3, 7), (5, 576), (33, 2048), (256, 1536), (17, 2304), (2, 8192)])
+@pytest.mark.parametrize("rows,hidden", [(1, 4), (3, 7), (5, 576), (33, 2048), (256, 1536), (17, 2304), (2, 8192),
+                                         (4093, 1536), (2050, 2048), (4100, 576)])
 @pytest.mark.parametrize("mode", ["plain", "residual", "addnorm", "addscale"])
 def test_rms_modes_ragged(rt, ora, rows, hidden, mode):
     inp, m = cases.rms_case(rows, hidden, 1e-6, 1000 + rows + hidden, mode)
