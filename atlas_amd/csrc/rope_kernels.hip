@@ -22,6 +22,8 @@
 #include "device_common.hpp"
 #include "launch.hpp"
 
+#include <stdlib.h>
+
 namespace atlas {
 namespace {
 
@@ -179,6 +181,163 @@ __global__ __launch_bounds__(64) void qk_norm_rope_kernel(
                          : q_out + (static_cast<size_t>(t) * q_heads + local) * D;
         stv<V>(dst + col, y);
     }
+}
+
+// Token engine (sequential order, the default for head_dim = 128*P): one
+// wavefront per token covers its q_heads Q rows and the optional K row
+// (U = q_heads + has_key <= MAXU units).  Lane l owns RoPE pairs
+// [l*P, l*P + P) of every unit and keeps both halves x[p] and x[p + d/2] in
+// registers, so the rotation needs no cross-lane exchange; the token's
+// cos/sin row and the four weight slices are loaded once per wavefront.
+// Loads are straight-line (units past U are clamped to a valid duplicate
+// address, never stored) and nontemporal; squares go to LDS and lane u folds
+// unit u in index order (bit-identical to the CPU composition
+// rms_norm -> rope).  Every unit is fully read before it is written, so
+// q_out == q and k_out == k are allowed.
+template <int P>
+struct pvec {
+    float v[P];
+};
+
+template <int P, bool NT>
+__device__ __forceinline__ pvec<P> ld_p(const float* p) {
+    constexpr bool nt = NT;
+    pvec<P> r;
+    if constexpr (P == 1) {
+        r.v[0] = nt ? __builtin_nontemporal_load(p) : *p;
+    } else if constexpr (P == 2) {
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        const f2 a = nt ? __builtin_nontemporal_load(reinterpret_cast<const f2*>(p)) : *reinterpret_cast<const f2*>(p);
+        r.v[0] = a.x;
+        r.v[1] = a.y;
+    } else {
+        typedef float f4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int j = 0; j < P; j += 4) {
+            const f4 a = nt ? __builtin_nontemporal_load(reinterpret_cast<const f4*>(p + j))
+                            : *reinterpret_cast<const f4*>(p + j);
+            r.v[j] = a.x;
+            r.v[j + 1] = a.y;
+            r.v[j + 2] = a.z;
+            r.v[j + 3] = a.w;
+        }
+    }
+    return r;
+}
+
+template <int P>
+__device__ __forceinline__ void st_p(float* p, const pvec<P>& r) {
+    if constexpr (P == 1) {
+        __builtin_nontemporal_store(r.v[0], p);
+    } else if constexpr (P == 2) {
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        __builtin_nontemporal_store(f2{r.v[0], r.v[1]}, reinterpret_cast<f2*>(p));
+    } else {
+        typedef float f4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int j = 0; j < P; j += 4)
+            __builtin_nontemporal_store(f4{r.v[j], r.v[j + 1], r.v[j + 2], r.v[j + 3]},
+                                        reinterpret_cast<f4*>(p + j));
+    }
+}
+
+template <int P>
+__device__ __forceinline__ void sq_p(float* dst, const pvec<P>& x) {
+#pragma unroll
+    for (int j = 0; j < P; ++j) dst[j] = x.v[j] * x.v[j];
+}
+
+template <int P, int MAXU>
+__global__ __launch_bounds__(64) void qk_norm_rope_token_kernel(
+    const float* q, const float* k, const float* q_weight, const float* k_weight, const float* cosine,
+    const float* sine, float* q_out, float* k_out, uint32_t q_heads, uint32_t has_key, uint32_t rope_stride,
+    float epsilon) {
+    constexpr uint32_t HALF = 64 * P;
+    constexpr uint32_t D = 2 * HALF;
+    constexpr uint32_t STRIDE = D + 4;
+    __shared__ float sq[MAXU * STRIDE];
+    const uint32_t lane = threadIdx.x;
+    const uint32_t t = blockIdx.x;
+    const uint32_t total = q_heads + has_key;
+    const uint32_t p0 = lane * P;
+
+    pvec<P> lo[MAXU], hi[MAXU];
+#pragma unroll
+    for (int u = 0; u < MAXU; ++u) {
+        const uint32_t uu = min(static_cast<uint32_t>(u), total - 1);
+        const float* src = uu >= q_heads ? k + static_cast<size_t>(t) * D
+                                         : q + (static_cast<size_t>(t) * q_heads + uu) * D;
+        lo[u] = ld_p<P, true>(src + p0);
+        hi[u] = ld_p<P, true>(src + HALF + p0);
+    }
+    const size_t tb = static_cast<size_t>(t) * rope_stride + p0;
+    const pvec<P> c = ld_p<P, false>(cosine + tb), s = ld_p<P, false>(sine + tb);
+    const pvec<P> qwl = ld_p<P, false>(q_weight + p0), qwh = ld_p<P, false>(q_weight + HALF + p0);
+    const float* kw = has_key ? k_weight : q_weight;
+    const pvec<P> kwl = ld_p<P, false>(kw + p0), kwh = ld_p<P, false>(kw + HALF + p0);
+
+#pragma unroll
+    for (int u = 0; u < MAXU; ++u) {
+        sq_p<P>(sq + u * STRIDE + p0, lo[u]);
+        sq_p<P>(sq + u * STRIDE + HALF + p0, hi[u]);
+    }
+    __syncthreads();
+    float sum = 0.0f;
+    if (lane < total) {
+        const float* row = sq + lane * STRIDE;
+#pragma unroll 8
+        for (uint32_t i = 0; i < D; i += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(row + i);
+            sum = sum + v.x;
+            sum = sum + v.y;
+            sum = sum + v.z;
+            sum = sum + v.w;
+        }
+    }
+    const float inv = lane < total ? inverse_rms(sum, static_cast<float>(D), epsilon) : 0.0f;
+
+#pragma unroll
+    for (int u = 0; u < MAXU; ++u) {
+        if (static_cast<uint32_t>(u) < total) {
+        const float iu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), u));
+        const bool key = static_cast<uint32_t>(u) >= q_heads;
+        pvec<P> ol, oh;
+#pragma unroll
+        for (int j = 0; j < P; ++j) {
+            const float wl = key ? kwl.v[j] : qwl.v[j];
+            const float wh = key ? kwh.v[j] : qwh.v[j];
+            const float x0 = lo[u].v[j] * iu * wl;
+            const float x1 = hi[u].v[j] * iu * wh;
+            ol.v[j] = x0 * c.v[j] - x1 * s.v[j];
+            oh.v[j] = x0 * s.v[j] + x1 * c.v[j];
+        }
+        float* dst = key ? k_out + static_cast<size_t>(t) * D : q_out + (static_cast<size_t>(t) * q_heads + u) * D;
+        st_p<P>(dst + p0, ol);
+        st_p<P>(dst + HALF + p0, oh);
+        }
+    }
+}
+
+template <int P>
+hipError_t launch_qk_token_p(hipStream_t s, const float* q, const float* k, const float* qw, const float* kw,
+                             const float* c, const float* sn, float* qo, float* ko, uint32_t tokens,
+                             uint32_t q_heads, uint32_t has_key, uint32_t rope_stride, float eps) {
+    const uint32_t total = q_heads + has_key;
+#define ATLAS_QK_CASE(U)                                                                                     \
+    if (total <= U) {                                                                                        \
+        hipLaunchKernelGGL((qk_norm_rope_token_kernel<P, U>), dim3(tokens), dim3(kWave), 0, s, q, k, qw, kw, \
+                           c, sn, qo, ko, q_heads, has_key, rope_stride, eps);                               \
+        return hipGetLastError();                                                                            \
+    }
+    ATLAS_QK_CASE(1)
+    ATLAS_QK_CASE(2)
+    ATLAS_QK_CASE(4)
+    ATLAS_QK_CASE(8)
+    ATLAS_QK_CASE(9)
+    ATLAS_QK_CASE(12)
+    ATLAS_QK_CASE(16)
+#undef ATLAS_QK_CASE
+    return hipErrorInvalidValue;
 }
 
 // Generic head_dim fallback (even head_dim not of the form 64*V): one wave
@@ -352,6 +511,14 @@ __global__ __launch_bounds__(256) void rope_interleaved_kernel(const float* x, c
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+bool qk_legacy_forced() {
+    static const bool forced = [] {
+        const char* v = getenv("ATLAS_QK_UNIT_ENGINE");
+        return v && *v && atoi(v) != 0;
+    }();
+    return forced;
+}
+
 template <int V, int UNITS>
 hipError_t launch_qk(hipStream_t s, bool seq, const float* q, const float* k, const float* qw,
                      const float* kw, const float* c, const float* sn, float* qo, float* ko,
@@ -377,7 +544,28 @@ hipError_t launch_qk_norm_rope_f32(hipStream_t stream, Reduction red, const floa
                                    uint32_t has_key, uint32_t head_dim, uint32_t rope_stride,
                                    float epsilon) {
     const bool seq = red == kSequential;
-    // Fast path: head_dim = 64*V, 16-byte aligned operands (8-byte for V=2),
+    // Token engine: head_dim = 128*P, at most 16 units per token, operands
+    // and per-token cos/sin rows aligned to P floats.
+    {
+        const uint32_t P = head_dim / 128;
+        const uintptr_t pa = 4u * (P == 0 ? 1 : P) > 16 ? 16 : 4u * (P == 0 ? 1 : P);
+        const bool ok = seq && head_dim % 128 == 0 && (P == 1 || P == 2 || P == 4) && q_heads + has_key <= 16 &&
+                        q_heads + has_key > 0 && aligned(q, pa) && aligned(q_out, pa) && aligned(q_weight, pa) &&
+                        aligned(cosine, pa) && aligned(sine, pa) && rope_stride % P == 0 &&
+                        (!has_key || (aligned(k, pa) && aligned(k_out, pa) && aligned(k_weight, pa))) &&
+                        !qk_legacy_forced();
+        if (ok) {
+            if (P == 1)
+                return launch_qk_token_p<1>(stream, q, k, q_weight, k_weight, cosine, sine, q_out, k_out, tokens,
+                                            q_heads, has_key, rope_stride, epsilon);
+            if (P == 2)
+                return launch_qk_token_p<2>(stream, q, k, q_weight, k_weight, cosine, sine, q_out, k_out, tokens,
+                                            q_heads, has_key, rope_stride, epsilon);
+            return launch_qk_token_p<4>(stream, q, k, q_weight, k_weight, cosine, sine, q_out, k_out, tokens,
+                                        q_heads, has_key, rope_stride, epsilon);
+        }
+    }
+    // Unit engine: head_dim = 64*V, 16-byte aligned operands (8-byte for V=2),
     // and per-token cos/sin rows aligned to the vector width.
     const uintptr_t va = head_dim == 128 ? 8 : 16;
     const bool vec_ok = (head_dim == 128 || head_dim == 256 || head_dim == 512) && aligned(q, va) &&
