@@ -220,7 +220,7 @@ def main():
 
     per_op = {}
     for name, (_, _, nbytes, launch) in ops.table.items():
-        if only and name not in only:
+        if (only or args.copy_mib) and name not in only:
             continue
         nsets = max(4, math.ceil(ROTATION_BYTES / ops.set_bytes(name)))
         log(f"timing {name} ({nsets} rotating sets)")
@@ -239,7 +239,7 @@ def main():
             rt.copy(dst, src, n)
         rt.sync()
         log(f"copied {args.copy_mib} MiB x5 (PMC calibration)")
-    if only:
+    if only or args.copy_mib:
         print(json.dumps({"per_op": per_op}))
         rt.close()
         return
