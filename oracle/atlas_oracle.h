@@ -8,7 +8,8 @@
  * load it; the product library (libatlas_hip_ops.so) never links or calls it.
  *
  * Arithmetic contract: IEEE-754 binary32, round-to-nearest-even, no FMA
- * contraction (built with -ffp-contract=off), fixed evaluation order that
+ * contraction (built with -ffp-contract=off; the only fused multiply-adds
+ * are the explicit fmaf calls of oracle_expf), fixed evaluation order that
  * restates the reference's Rust CPU oracles and Metal kernels, cited per
  * function as `path:line` into the bisegni/atlas tree.
  *
