@@ -332,3 +332,63 @@ def test_wide_reduction_is_tolerance_level(rt, ora):
             assert np.linalg.norm(g_ - e_) / np.linalg.norm(e_) <= 1e-6
     finally:
         rt.set_reduction(ATLAS_REDUCTION_SEQUENTIAL)
+
+
+def _adversarial_rows(rows, hidden, seed):
+    """Rows that stress the exact wave-parallel fold of the sum of squares:
+    rounding ties, binade crossings, zeros, subnormal and overflowing squares,
+    non-finite values and wide exponent ranges."""
+    r = np.random.default_rng(seed)
+    x = r.standard_normal((rows, hidden)).astype(f32)
+    for i in range(rows):
+        kind = i % 16
+        row = x[i]
+        if kind == 1:
+            row *= f32(1e-20)                                   # subnormal squares
+        elif kind == 2:
+            row *= f32(1e18)                                    # sum overflows to inf
+        elif kind == 3:
+            row[r.random(hidden) < 0.5] = 0.0                   # many zeros
+        elif kind == 4:
+            row[:] = np.trunc(row * 4) / 4                      # coarse values: many exact ties
+        elif kind == 5:
+            row[7] = np.inf
+        elif kind == 6:
+            row[hidden // 3] = np.nan
+        elif kind == 7:
+            row[:] = 1.0
+        elif kind == 8:
+            row[:] = (np.arange(hidden) % 7) * f32(0.5)
+        elif kind == 9:
+            row[:100] *= f32(1e-3)                              # slow start
+        elif kind == 10:
+            row[:] = np.ldexp(1.0 + r.random(hidden), r.integers(-20, 20, hidden)).astype(f32)
+        elif kind == 11:
+            row[:] = 0.0
+        elif kind == 12:
+            row[:] = np.sqrt(np.ldexp(1.0, r.integers(0, 8, hidden))).astype(f32)
+        elif kind == 13:
+            row *= f32(1e-6)
+        elif kind == 14:
+            row[:] = np.trunc(row * 64) / 64
+    return x.reshape(-1)
+
+
+def _assert_bits_nan_equal(name, got, exp):
+    for i, (g, e) in enumerate(zip(got, exp)):
+        g, e = np.asarray(g).reshape(-1), np.asarray(e).reshape(-1)
+        same = (g.view(np.uint32) == e.view(np.uint32)) | (np.isnan(g) & np.isnan(e))
+        if not same.all():
+            j = int(np.nonzero(~same)[0][0])
+            raise AssertionError(f"{name}[{i}]: {int((~same).sum())} of {g.size} differ; first at {j}: "
+                                 f"gpu={g[j]!r} oracle={e[j]!r}")
+
+
+@pytest.mark.parametrize("hidden", [1536, 2048, 576, 1024, 260])
+@pytest.mark.parametrize("mode", ["plain", "residual", "addnorm", "addscale"])
+def test_rms_exact_fold_adversarial_rows(rt, ora, hidden, mode):
+    rows = 2048 + 48   # R = 2 path (and its ragged tail), every row kind many times
+    inp, m = cases.rms_case(rows, hidden, 1e-6, 4000 + hidden, mode)
+    inp["x"] = _adversarial_rows(rows, hidden, 5000 + hidden)
+    say(f"rms exact fold adversarial {mode} rows={rows} hidden={hidden}")
+    _assert_bits_nan_equal(f"rms_{mode}", cases.rms_gpu(rt, inp, m), cases.rms_oracle(ora, inp, m))
