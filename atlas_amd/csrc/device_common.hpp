@@ -23,6 +23,8 @@ __device__ __forceinline__ float fdiv_rn(float a, float b) { return a / b; }
 // default -fhip-fp32-correctly-rounded-divide-sqrt.
 __device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ float pow2i(int k) {  // 2^k, k in [-126, 127]
     return __uint_as_float(static_cast<uint32_t>(k + 127) << 23);
 }
@@ -99,6 +101,46 @@ __device__ __forceinline__ float materialize(float v) {
 
 __device__ __forceinline__ uint16_t f2h(float v) {  // IEEE RNE of the f32 value
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(materialize(v)));
+}
+
+// Sequential f32 fold of n4 (<= 64) float4 of squares from LDS into s, in
+// index order.  A full chunk is straight-line code in groups of 8 float4:
+// the next group's reads are issued before the current group's 32 adds, so
+// LDS latency hides under the dependent add chain (~8 cycles per add).
+__device__ __forceinline__ float fold_lds_chunk(const f32x4* p, uint32_t n4, float s) {
+    if (n4 == 64) {
+        f32x4 cur[8], nxt[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) cur[i] = p[i];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            if (g < 7) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) nxt[i] = p[8 * (g + 1) + i];
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                s = s + cur[i].x;
+                s = s + cur[i].y;
+                s = s + cur[i].z;
+                s = s + cur[i].w;
+            }
+            if (g < 7) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+            }
+        }
+        return s;
+    }
+#pragma unroll 8
+    for (uint32_t k = 0; k < n4; ++k) {
+        const f32x4 v = p[k];
+        s = s + v.x;
+        s = s + v.y;
+        s = s + v.z;
+        s = s + v.w;
+    }
+    return s;
 }
 
 }  // namespace atlas

@@ -222,8 +222,6 @@ __global__ __launch_bounds__(256) void rms_wide_kernel(NormArgs a) {
 // Each row is fully read before any of its outputs is written, so the
 // aliased bindings of the reference call sites stay valid.
 // ---------------------------------------------------------------------------
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ f32x4 ldg_nt(const float* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
 }
@@ -232,45 +230,6 @@ __device__ __forceinline__ void stg_nt(float* p, f32x4 v) {
     __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
 }
 
-// Sequential f32 fold of n4 (<= 64) float4 of squares from LDS into s, in
-// index order.  A full chunk is straight-line code in groups of 8 float4:
-// the next group's reads are issued before the current group's 32 adds, so
-// LDS latency hides under the dependent add chain (~8 cycles per add).
-__device__ __forceinline__ float fold_lds_chunk(const f32x4* p, uint32_t n4, float s) {
-    if (n4 == 64) {
-        f32x4 cur[8], nxt[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) cur[i] = p[i];
-#pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            if (g < 7) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) nxt[i] = p[8 * (g + 1) + i];
-            }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                s = s + cur[i].x;
-                s = s + cur[i].y;
-                s = s + cur[i].z;
-                s = s + cur[i].w;
-            }
-            if (g < 7) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
-            }
-        }
-        return s;
-    }
-#pragma unroll 8
-    for (uint32_t k = 0; k < n4; ++k) {
-        const f32x4 v = p[k];
-        s = s + v.x;
-        s = s + v.y;
-        s = s + v.z;
-        s = s + v.w;
-    }
-    return s;
-}
 
 template <int R, int J, int MODE>
 __global__ __launch_bounds__(64) void rms_reg_kernel(NormArgs a) {

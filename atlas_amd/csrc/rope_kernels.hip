@@ -255,7 +255,7 @@ __global__ __launch_bounds__(64) void qk_norm_rope_token_kernel(
     constexpr uint32_t HALF = 64 * P;
     constexpr uint32_t D = 2 * HALF;
     constexpr uint32_t STRIDE = D + 4;
-    __shared__ float sq[MAXU * STRIDE];
+    __shared__ __align__(16) float sq[MAXU * STRIDE];
     const uint32_t lane = threadIdx.x;
     const uint32_t t = blockIdx.x;
     const uint32_t total = q_heads + has_key;
@@ -284,15 +284,9 @@ __global__ __launch_bounds__(64) void qk_norm_rope_token_kernel(
     __syncthreads();
     float sum = 0.0f;
     if (lane < total) {
-        const float* row = sq + lane * STRIDE;
-#pragma unroll 8
-        for (uint32_t i = 0; i < D; i += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(row + i);
-            sum = sum + v.x;
-            sum = sum + v.y;
-            sum = sum + v.z;
-            sum = sum + v.w;
-        }
+        const f32x4* row = reinterpret_cast<const f32x4*>(sq + lane * STRIDE);
+#pragma unroll
+        for (uint32_t c = 0; c < D / 4; c += 64) sum = fold_lds_chunk(row + c, D / 4 - c < 64 ? D / 4 - c : 64, sum);
     }
     const float inv = lane < total ? inverse_rms(sum, static_cast<float>(D), epsilon) : 0.0f;
 
