@@ -70,6 +70,10 @@ SIGNATURES = {
     "atlas_hip_event_record": [CTX, P],
     "atlas_hip_event_elapsed_ms": [CTX, P, P, POINTER(c_float)],
     "atlas_hip_event_destroy": [CTX, P],
+    "atlas_hip_graph_begin": [CTX],
+    "atlas_hip_graph_end": [CTX, POINTER(c_void_p)],
+    "atlas_hip_graph_launch": [CTX, P],
+    "atlas_hip_graph_destroy": [CTX, P],
     "atlas_hip_rms_norm_f32": [CTX, P, P, P, U32, U32, F],
     "atlas_hip_rms_norm_residual_f32": [CTX, P, P, P, P, P, U32, U32, F],
     "atlas_hip_add_rms_norm_f32": [CTX, P, P, P, P, P, U32, U32, F],

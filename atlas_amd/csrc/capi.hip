@@ -22,6 +22,7 @@ struct atlas_hip_ctx {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     int reduction = ATLAS_REDUCTION_SEQUENTIAL;
+    bool capturing = false;
     std::string last_error;
     atlas_hip_telemetry tel{};
 };
@@ -129,6 +130,7 @@ void atlas_hip_destroy(atlas_hip_ctx* ctx) {
 int atlas_hip_sync(atlas_hip_ctx* ctx) {
     int rc = enter(ctx);
     if (rc) return rc;
+    if (ctx->capturing) return invalid(ctx, "not allowed while a graph capture is open");
     hipError_t e = hipStreamSynchronize(ctx->stream);
     ctx->tel.syncs += 1;
     if (e != hipSuccess) return hip_fail(ctx, e, "command failed");
@@ -168,6 +170,7 @@ int atlas_hip_get_telemetry(const atlas_hip_ctx* ctx, atlas_hip_telemetry* out) 
 int atlas_hip_malloc(atlas_hip_ctx* ctx, size_t bytes, void** ptr) {
     int rc = enter(ctx);
     if (rc) return rc;
+    if (ctx->capturing) return invalid(ctx, "not allowed while a graph capture is open");
     if (!ptr) return invalid(ctx, "null output pointer");
     *ptr = nullptr;
     hipError_t e = hipMalloc(ptr, bytes ? bytes : 16);
@@ -194,6 +197,7 @@ int atlas_hip_free(atlas_hip_ctx* ctx, void* ptr) {
 int atlas_hip_upload(atlas_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
     int rc = enter(ctx);
     if (rc) return rc;
+    if (ctx->capturing) return invalid(ctx, "not allowed while a graph capture is open");
     if (!bytes) return ATLAS_OK;
     if (!dst || !src) return invalid(ctx, "null upload pointer");
     hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream);
@@ -206,6 +210,7 @@ int atlas_hip_upload(atlas_hip_ctx* ctx, void* dst, const void* src, size_t byte
 int atlas_hip_download(atlas_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
     int rc = enter(ctx);
     if (rc) return rc;
+    if (ctx->capturing) return invalid(ctx, "not allowed while a graph capture is open");
     if (!bytes) return ATLAS_OK;
     if (!dst || !src) return invalid(ctx, "null download pointer");
     hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream);
@@ -218,6 +223,7 @@ int atlas_hip_download(atlas_hip_ctx* ctx, void* dst, const void* src, size_t by
 int atlas_hip_memset(atlas_hip_ctx* ctx, void* dst, int value, size_t bytes) {
     int rc = enter(ctx);
     if (rc) return rc;
+    if (ctx->capturing) return invalid(ctx, "not allowed while a graph capture is open");
     if (!bytes) return ATLAS_OK;
     if (!dst) return invalid(ctx, "null memset pointer");
     hipError_t e = hipMemsetAsync(dst, value, bytes, ctx->stream);
@@ -228,6 +234,7 @@ int atlas_hip_memset(atlas_hip_ctx* ctx, void* dst, int value, size_t bytes) {
 int atlas_hip_copy_d2d(atlas_hip_ctx* ctx, void* dst, const void* src, size_t bytes) {
     int rc = enter(ctx);
     if (rc) return rc;
+    if (ctx->capturing) return invalid(ctx, "not allowed while a graph capture is open");
     if (!bytes) return ATLAS_OK;
     if (!dst || !src) return invalid(ctx, "null copy pointer");
     hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream);
@@ -269,6 +276,58 @@ int atlas_hip_event_destroy(atlas_hip_ctx* ctx, void* event) {
     if (rc) return rc;
     hipError_t e = hipEventDestroy(static_cast<hipEvent_t>(event));
     if (e != hipSuccess) return hip_fail(ctx, e, "hipEventDestroy");
+    return ATLAS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// graph capture
+// ---------------------------------------------------------------------------
+
+int atlas_hip_graph_begin(atlas_hip_ctx* ctx) {
+    int rc = enter(ctx);
+    if (rc) return rc;
+    if (ctx->capturing) return invalid(ctx, "a graph capture is already open on this context");
+    hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamBeginCapture");
+    ctx->capturing = true;
+    return ATLAS_OK;
+}
+
+int atlas_hip_graph_end(atlas_hip_ctx* ctx, void** graph) {
+    int rc = enter(ctx);
+    if (rc) return rc;
+    if (!graph) return invalid(ctx, "null graph pointer");
+    *graph = nullptr;
+    if (!ctx->capturing) return invalid(ctx, "no graph capture is open on this context");
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphInstantiate");
+    *graph = exec;
+    return ATLAS_OK;
+}
+
+int atlas_hip_graph_launch(atlas_hip_ctx* ctx, void* graph) {
+    int rc = enter(ctx);
+    if (rc) return rc;
+    if (!graph) return invalid(ctx, "null graph");
+    if (ctx->capturing) return invalid(ctx, "cannot launch a graph while capturing");
+    hipError_t e = hipGraphLaunch(static_cast<hipGraphExec_t>(graph), ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphLaunch");
+    ctx->tel.dispatches += 1;
+    return ATLAS_OK;
+}
+
+int atlas_hip_graph_destroy(atlas_hip_ctx* ctx, void* graph) {
+    int rc = enter(ctx);
+    if (rc) return rc;
+    if (!graph) return ATLAS_OK;
+    hipError_t e = hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph));
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphExecDestroy");
     return ATLAS_OK;
 }
 

@@ -162,6 +162,23 @@ class HipRuntime:
         self._check(self.lib.atlas_hip_event_elapsed_ms(self.ctx, start, stop, byref(ms)))
         return ms.value
 
+    # -- graph capture ---------------------------------------------------
+    def graph_begin(self) -> None:
+        """Start recording the ops enqueued on this context (atlas_hip_graph_begin)."""
+        self._check(self.lib.atlas_hip_graph_begin(self.ctx))
+
+    def graph_end(self) -> int:
+        """Finish recording; returns an executable graph handle."""
+        g = c_void_p()
+        self._check(self.lib.atlas_hip_graph_end(self.ctx, byref(g)))
+        return g.value
+
+    def graph_launch(self, graph: int) -> None:
+        self._check(self.lib.atlas_hip_graph_launch(self.ctx, graph))
+
+    def graph_destroy(self, graph: int) -> None:
+        self._check(self.lib.atlas_hip_graph_destroy(self.ctx, graph))
+
     # -- resident (device-pointer) ops ----------------------------------
     def rms_norm(self, x, w, y, rows, hidden, eps):
         self._check(self.lib.atlas_hip_rms_norm_f32(self.ctx, _ptr(x), _ptr(w), _ptr(y), rows, hidden, eps))

@@ -23,8 +23,9 @@ reference CPU operators) timed on this host over a bounded token sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--reduction sequential|wide]
        python bench.py --only geglu,rms_norm        (per-op timing only, for profiling)
-       python bench.py --only geglu --copy-mib 512  (plus a D2D copy of known size,
-                                                      the PMC calibration kernel)
+       python bench.py --copy-mib 256               (a D2D copy of known size: the PMC
+                                                      calibration kernel)
+       python bench.py --decode                     (configs[4] batched decode, separate line)
 """
 import argparse
 import json
@@ -176,6 +177,53 @@ def cpu_baseline(wl, budget_s=10.0):
                       f"(-O2, -ffp-contract=off), same op list and per-token shapes (gather vocab 4096)"}
 
 
+def decode_bench(rt, steps, warmup):
+    """256 sequences x 1 token, 35 layers of the fused ops in
+    the reference decode order (atlas_amd.decode), eager and as one HIP graph."""
+    from atlas_amd import workloads as wl
+    from atlas_amd.decode import GemmaDecodeStep
+
+    S = wl.DecodeShape()
+    log("building the decode step (35 layers of seeded weights and stand-ins)")
+    step = GemmaDecodeStep(rt, S, seed=5)
+
+    def timed(fn, n):
+        for _ in range(warmup):
+            fn()
+        rt.sync()
+        a, b = rt.event(), rt.event()
+        rt.record(a)
+        for _ in range(n):
+            fn()
+        rt.record(b)
+        rt.sync()
+        return rt.elapsed_ms(a, b) * 1e3 / n
+
+    eager_us = timed(step.enqueue, steps)
+    step.capture()
+    graph_us = timed(step.replay, steps)
+    d, o, H, L, W = step.dev, step.out, S.hidden, S.layers, S.ple_width
+
+    def head():
+        rt.embed_q4_0(d["token_table"], d["ids"], o["state"], step.vocab, H, S.batch, wl.f32_sqrt(H))
+        rt.ple_q4_0(d["ple_table"], d["ids"], d["ple_proj_in"], o["ple"], step.vocab, L, W, S.batch, 16.0,
+                    wl.SQRT_2_RECIP)
+
+    head_us = timed(head, steps)
+    step.close()
+    per_layer = (graph_us - head_us) / L
+    return {"metric": "C5 batched decode: per-layer latency of the fused ops (graph replay), 1 GPU",
+            "value": round(per_layer, 3), "unit": "us/layer", "higher_is_better": False, "n_gpus": 1,
+            "steps": steps, "warmup": warmup, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "gemma4-e2b-batched-decode (configs[4])", "sequences": S.batch,
+                       "layers": L, "hidden": H, "ffn": S.ffn, "q_heads": S.q_heads, "head_dim": S.head_dim,
+                       "theta": "1e4 local / 1e6 global, 4:1", "ops_per_layer": 6},
+            "step_us_graph": round(graph_us, 2), "step_us_eager": round(eager_us, 2),
+            "embed_ple_us": round(head_us, 2), "bytes_per_layer": step.bytes_per_layer(),
+            "layer_GB/s": round(step.bytes_per_layer() / (per_layer * 1e-6) / 1e9, 1),
+            "step_GB/s": round(step.bytes_per_step() / (graph_us * 1e-6) / 1e9, 1)}
+
+
 def pmc_traffic(kernel_op):
     """HBM bytes per launch from the committed rocprofv3 PMC summary, or None."""
     path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
@@ -200,6 +248,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma-separated op subset: per-op timing only (profiling)")
     ap.add_argument("--copy-mib", type=int, default=0, help="also time a device-to-device copy of this size")
+    ap.add_argument("--decode", action="store_true",
+                    help="BASELINE configs[4] batched decode (per-layer latency, eager and HIP graph) instead")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every op of this path is row-independent and this build "
@@ -211,6 +261,10 @@ def main():
     from atlas_amd import workloads as wl
 
     rt = HipRuntime(0, ATLAS_REDUCTION_WIDE if args.reduction == "wide" else ATLAS_REDUCTION_SEQUENTIAL)
+    if args.decode:
+        print(json.dumps(decode_bench(rt, min(args.steps, 50), min(args.warmup, 5))))
+        rt.close()
+        return
     ops = Ops(wl, rope_tables_gemma4)
     T = ops.L.tokens
     only = [o for o in args.only.split(",") if o]

@@ -108,6 +108,23 @@ int atlas_hip_event_record(atlas_hip_ctx *ctx, void *event);
 int atlas_hip_event_elapsed_ms(atlas_hip_ctx *ctx, void *start, void *stop, float *ms);
 int atlas_hip_event_destroy(atlas_hip_ctx *ctx, void *event);
 
+/* ---- graph capture (replaces re-encoding a ResidentCommand per token) ---- */
+
+/* The reference encodes every dispatch of a decode token into a fresh Metal
+ * command buffer each token (begin_resident_command, lib.rs:1232-1253;
+ * gemma4_executor.rs:4123-4690).  On MI355X the executor instead records the
+ * chain once and replays it: atlas_hip_graph_begin starts capturing the
+ * context stream, every atlas_hip_* op enqueued until atlas_hip_graph_end is
+ * recorded (not run), and atlas_hip_graph_launch replays the whole chain with
+ * one submission.  Kernel arguments are frozen at capture time, so per-token
+ * values must live in device buffers (as the reference's scalar buffers do,
+ * gemma4_executor.rs:1852-1895).  While capturing, call only device-pointer
+ * ops: no atlas_ops_*, sync, upload, download, memset or copy. */
+int atlas_hip_graph_begin(atlas_hip_ctx *ctx);
+int atlas_hip_graph_end(atlas_hip_ctx *ctx, void **graph);
+int atlas_hip_graph_launch(atlas_hip_ctx *ctx, void *graph);
+int atlas_hip_graph_destroy(atlas_hip_ctx *ctx, void *graph);
+
 /* ---- RMSNorm family (device pointers, async) ---------------------------- */
 
 /* rms_norm_f32 / rms_norm_decode_batch_f32 (kernels.metal:106-133); caller
