@@ -557,6 +557,144 @@ __global__ __launch_bounds__(64) void rms_f16_seq_kernel(const uint16_t* x, cons
     }
 }
 
+// ---------------------------------------------------------------------------
+// FP16-storage register engine (sequential order, 16-byte aligned rows with
+// hidden % 8 == 0 and hidden <= 4096).  Same structure as rms_reg_kernel:
+// lane l keeps 8 halves (one 128-bit load) of column l + 64*j of each row;
+// math is f32 on exactly widened values; outputs are rounded RNE once.  With
+// ADD the stored residual stream rne16(x + residual) is what is squared and
+// normalised, matching the two-kernel chain with f16 buffers.
+// ---------------------------------------------------------------------------
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float lo16(uint32_t w) { return h2f(static_cast<uint16_t>(w)); }
+__device__ __forceinline__ float hi16(uint32_t w) { return h2f(static_cast<uint16_t>(w >> 16)); }
+__device__ __forceinline__ uint32_t pack16(float lo, float hi) {
+    return static_cast<uint32_t>(f2h(lo)) | (static_cast<uint32_t>(f2h(hi)) << 16);
+}
+
+template <int R, int J, bool ADD>
+__global__ __launch_bounds__(64) void rms_reg_f16_kernel(const uint16_t* x, const uint16_t* residual,
+                                                         const uint16_t* weight, uint16_t* residual_out,
+                                                         uint16_t* out, uint32_t rows, uint32_t hidden,
+                                                         float epsilon) {
+    extern __shared__ f32x4 sq4[];  // R rows x (hidden/4 + 1) float4 of squares
+    const uint32_t lane = threadIdx.x;
+    const uint32_t n8 = hidden >> 3;          // 8-half groups per row
+    const uint32_t stride4 = (hidden >> 2) + 1;
+    const uint32_t row0 = blockIdx.x * R;
+    const uint32_t nrows = min(static_cast<uint32_t>(R), rows - row0);
+
+    u32x4 xv[R][J];
+    u32x4 ev[ADD ? R : 1][ADD ? J : 1];
+    u32x4 wv[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t c = min(lane + 64u * j, n8 - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const size_t idx = static_cast<size_t>(row0 + min(static_cast<uint32_t>(r), nrows - 1)) * hidden + 8 * c;
+            xv[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + idx));
+            if (ADD) ev[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(residual + idx));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+        wv[j] = *reinterpret_cast<const u32x4*>(weight + 8 * min(lane + 64u * j, n8 - 1));
+
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const uint32_t c = min(lane + 64u * j, n8 - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            u32x4 v = xv[r][j];
+            if (ADD) {
+                const u32x4 b = ev[r][j];
+                v = u32x4{pack16(lo16(v.x) + lo16(b.x), hi16(v.x) + hi16(b.x)),
+                          pack16(lo16(v.y) + lo16(b.y), hi16(v.y) + hi16(b.y)),
+                          pack16(lo16(v.z) + lo16(b.z), hi16(v.z) + hi16(b.z)),
+                          pack16(lo16(v.w) + lo16(b.w), hi16(v.w) + hi16(b.w))};
+                xv[r][j] = v;
+            }
+            const float a0 = lo16(v.x), a1 = hi16(v.x), a2 = lo16(v.y), a3 = hi16(v.y);
+            const float a4 = lo16(v.z), a5 = hi16(v.z), a6 = lo16(v.w), a7 = hi16(v.w);
+            sq4[r * stride4 + 2 * c] = f32x4{a0 * a0, a1 * a1, a2 * a2, a3 * a3};
+            sq4[r * stride4 + 2 * c + 1] = f32x4{a4 * a4, a5 * a5, a6 * a6, a7 * a7};
+        }
+        __syncthreads();
+        if (lane < nrows) {
+            const uint32_t begin = 128u * j, end = min(2 * n8, 128u * (j + 1));
+            const f32x4* row = sq4 + lane * stride4;
+            for (uint32_t k = begin; k < end; k += 64) s = fold_lds_chunk(row + k, min(64u, end - k), s);
+        }
+    }
+    if (ADD) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (static_cast<uint32_t>(r) >= nrows) break;
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const uint32_t c = lane + 64u * j;
+                if (c < n8)
+                    __builtin_nontemporal_store(
+                        xv[r][j], reinterpret_cast<u32x4*>(residual_out + static_cast<size_t>(row0 + r) * hidden + 8 * c));
+            }
+        }
+    }
+    const float inv = lane < nrows ? inverse_rms(s, static_cast<float>(hidden), epsilon) : 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (static_cast<uint32_t>(r) >= nrows) break;
+        const float ir = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t c = lane + 64u * j;
+            if (c >= n8) continue;
+            const u32x4 v = xv[r][j], w = wv[j];
+            const u32x4 y{pack16(lo16(v.x) * ir * lo16(w.x), hi16(v.x) * ir * hi16(w.x)),
+                          pack16(lo16(v.y) * ir * lo16(w.y), hi16(v.y) * ir * hi16(w.y)),
+                          pack16(lo16(v.z) * ir * lo16(w.z), hi16(v.z) * ir * hi16(w.z)),
+                          pack16(lo16(v.w) * ir * lo16(w.w), hi16(v.w) * ir * hi16(w.w))};
+            __builtin_nontemporal_store(y, reinterpret_cast<u32x4*>(out + static_cast<size_t>(row0 + r) * hidden + 8 * c));
+        }
+    }
+}
+
+template <int R, int J, bool ADD>
+hipError_t launch_f16_reg_rj(hipStream_t s, const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
+                             uint16_t* residual_out, uint16_t* out, uint32_t rows, uint32_t hidden, float eps) {
+    const size_t lds = static_cast<size_t>(R) * (hidden / 4 + 1) * sizeof(f32x4);
+    hipLaunchKernelGGL((rms_reg_f16_kernel<R, J, ADD>), dim3((rows + R - 1) / R), dim3(kWave), lds, s, x, residual,
+                       weight, residual_out, out, rows, hidden, eps);
+    return hipGetLastError();
+}
+
+template <int R, bool ADD>
+hipError_t launch_f16_reg_r(hipStream_t s, int J, const uint16_t* x, const uint16_t* residual,
+                            const uint16_t* weight, uint16_t* residual_out, uint16_t* out, uint32_t rows,
+                            uint32_t hidden, float eps) {
+    switch (J) {
+        case 1: return launch_f16_reg_rj<R, 1, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
+        case 2: return launch_f16_reg_rj<R, 2, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
+        case 3: return launch_f16_reg_rj<R, 3, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
+        case 4: return launch_f16_reg_rj<R, 4, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
+        case 5: return launch_f16_reg_rj<R, 5, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
+        case 6: return launch_f16_reg_rj<R, 6, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
+        case 7: return launch_f16_reg_rj<R, 7, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
+        default: return launch_f16_reg_rj<R, 8, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
+    }
+}
+
+template <bool ADD>
+hipError_t launch_f16_reg(hipStream_t s, const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
+                          uint16_t* residual_out, uint16_t* out, uint32_t rows, uint32_t hidden, float eps) {
+    const int J = static_cast<int>((hidden / 8 + 63) / 64);
+    if (pick_reg_rows(rows, J, 0) == 2)
+        return launch_f16_reg_r<2, ADD>(s, J, x, residual, weight, residual_out, out, rows, hidden, eps);
+    return launch_f16_reg_r<1, ADD>(s, J, x, residual, weight, residual_out, out, rows, hidden, eps);
+}
+
 }  // namespace
 
 hipError_t launch_rms_norm_f32(hipStream_t stream, NormMode mode, Reduction red, const NormArgs& a) {
@@ -602,6 +740,14 @@ hipError_t launch_rms_norm_f16(hipStream_t stream, Reduction red, const uint16_t
                                uint16_t* residual_out, uint16_t* out, uint32_t rows,
                                uint32_t hidden, float epsilon) {
     const int seq = red == kSequential ? 1 : 0;
+    const bool reg = seq && hidden % 8 == 0 && hidden <= 4096 && aligned16(x) && aligned16(weight) &&
+                     aligned16(out) && (!residual || (aligned16(residual) && aligned16(residual_out))) &&
+                     !lds_engine_forced();
+    if (reg) {
+        if (residual)
+            return launch_f16_reg<true>(stream, x, residual, weight, residual_out, out, rows, hidden, epsilon);
+        return launch_f16_reg<false>(stream, x, residual, weight, residual_out, out, rows, hidden, epsilon);
+    }
     const size_t lds = seq ? static_cast<size_t>(hidden) * sizeof(float) : 0;
     if (residual)
         hipLaunchKernelGGL((rms_f16_seq_kernel<true>), dim3(rows), dim3(kWave), lds, stream, x,

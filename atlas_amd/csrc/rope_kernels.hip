@@ -384,7 +384,28 @@ __global__ __launch_bounds__(64) void qk_norm_rope_generic_kernel(
     }
 }
 
-// Half-split RoPE, 4 pairs per thread when half % 4 == 0, else 1.
+// Half-split RoPE.  Each thread rotates P consecutive pairs of one
+// (token, head): x[p..p+P) and x[p+d/2..p+d/2+P) with cos/sin[t*stride + p..]
+// -- 128-bit accesses for the vector forms (P = 4 f32, P = 8 f16),
+// nontemporal for the streamed rows, cached for the per-token tables that
+// every head of the token reuses.
+template <int P>
+__device__ __forceinline__ void ld_tab(const float* p, float* dst) {
+    if constexpr (P % 4 == 0) {
+#pragma unroll
+        for (int j = 0; j < P; j += 4) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(p + j);
+            dst[j] = v.x;
+            dst[j + 1] = v.y;
+            dst[j + 2] = v.z;
+            dst[j + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < P; ++j) dst[j] = p[j];
+    }
+}
+
 template <int P>
 __global__ __launch_bounds__(256) void rope_half_f32_kernel(const float* x, const float* cosine,
                                                             const float* sine, float* out,
@@ -399,22 +420,19 @@ __global__ __launch_bounds__(256) void rope_half_f32_kernel(const float* x, cons
     const uint32_t p = static_cast<uint32_t>(i % groups_per_unit) * P;
     const uint32_t t = static_cast<uint32_t>(unit / heads);
     const size_t base = unit * head_dim;
-    const size_t tb = static_cast<size_t>(t) * rope_stride + p;
     float a[P], b[P], c[P], s[P];
     if constexpr (P == 4) {
-        float4 va = *reinterpret_cast<const float4*>(x + base + p);
-        float4 vb = *reinterpret_cast<const float4*>(x + base + p + half);
+        const f32x4 va = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + base + p));
+        const f32x4 vb = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(x + base + p + half));
         a[0] = va.x; a[1] = va.y; a[2] = va.z; a[3] = va.w;
         b[0] = vb.x; b[1] = vb.y; b[2] = vb.z; b[3] = vb.w;
     } else {
         a[0] = x[base + p];
         b[0] = x[base + p + half];
     }
-#pragma unroll
-    for (int j = 0; j < P; ++j) {
-        c[j] = cosine[tb + j];
-        s[j] = sine[tb + j];
-    }
+    const size_t tb = static_cast<size_t>(t) * rope_stride + p;
+    ld_tab<P>(cosine + tb, c);
+    ld_tab<P>(sine + tb, s);
     float o0[P], o1[P];
 #pragma unroll
     for (int j = 0; j < P; ++j) {
@@ -422,17 +440,16 @@ __global__ __launch_bounds__(256) void rope_half_f32_kernel(const float* x, cons
         o1[j] = a[j] * s[j] + b[j] * c[j];
     }
     if constexpr (P == 4) {
-        *reinterpret_cast<float4*>(out + base + p) = make_float4(o0[0], o0[1], o0[2], o0[3]);
-        *reinterpret_cast<float4*>(out + base + p + half) = make_float4(o1[0], o1[1], o1[2], o1[3]);
+        __builtin_nontemporal_store(f32x4{o0[0], o0[1], o0[2], o0[3]}, reinterpret_cast<f32x4*>(out + base + p));
+        __builtin_nontemporal_store(f32x4{o1[0], o1[1], o1[2], o1[3]},
+                                    reinterpret_cast<f32x4*>(out + base + p + half));
     } else {
         out[base + p] = o0[0];
         out[base + p + half] = o1[0];
     }
 }
 
-struct h4 {
-    uint16_t v[4];
-};
+typedef uint32_t u32x4r __attribute__((ext_vector_type(4)));
 
 template <int P>
 __global__ __launch_bounds__(256) void rope_half_f16_kernel(const uint16_t* x, const float* cosine,
@@ -448,37 +465,45 @@ __global__ __launch_bounds__(256) void rope_half_f16_kernel(const uint16_t* x, c
     const uint32_t p = static_cast<uint32_t>(i % groups_per_unit) * P;
     const uint32_t t = static_cast<uint32_t>(unit / heads);
     const size_t base = unit * head_dim;
-    const size_t tb = static_cast<size_t>(t) * rope_stride + p;
     uint16_t a[P], b[P];
-    if constexpr (P == 4) {
-        h4 va = *reinterpret_cast<const h4*>(x + base + p);
-        h4 vb = *reinterpret_cast<const h4*>(x + base + p + half);
+    if constexpr (P == 8) {
+        const u32x4r va = __builtin_nontemporal_load(reinterpret_cast<const u32x4r*>(x + base + p));
+        const u32x4r vb = __builtin_nontemporal_load(reinterpret_cast<const u32x4r*>(x + base + p + half));
+        const uint32_t wa[4] = {va.x, va.y, va.z, va.w}, wb[4] = {vb.x, vb.y, vb.z, vb.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            a[j] = va.v[j];
-            b[j] = vb.v[j];
+            a[2 * j] = static_cast<uint16_t>(wa[j]);
+            a[2 * j + 1] = static_cast<uint16_t>(wa[j] >> 16);
+            b[2 * j] = static_cast<uint16_t>(wb[j]);
+            b[2 * j + 1] = static_cast<uint16_t>(wb[j] >> 16);
         }
     } else {
         a[0] = x[base + p];
         b[0] = x[base + p + half];
     }
+    const size_t tb = static_cast<size_t>(t) * rope_stride + p;
+    float c[P], s[P];
+    ld_tab<P>(cosine + tb, c);
+    ld_tab<P>(sine + tb, s);
     uint16_t o0[P], o1[P];
 #pragma unroll
     for (int j = 0; j < P; ++j) {
         const float x0 = h2f(a[j]), x1 = h2f(b[j]);
-        const float c = cosine[tb + j], s = sine[tb + j];
-        o0[j] = f2h(x0 * c - x1 * s);
-        o1[j] = f2h(x0 * s + x1 * c);
+        o0[j] = f2h(x0 * c[j] - x1 * s[j]);
+        o1[j] = f2h(x0 * s[j] + x1 * c[j]);
     }
-    if constexpr (P == 4) {
-        h4 r0, r1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            r0.v[j] = o0[j];
-            r1.v[j] = o1[j];
-        }
-        *reinterpret_cast<h4*>(out + base + p) = r0;
-        *reinterpret_cast<h4*>(out + base + p + half) = r1;
+    if constexpr (P == 8) {
+        u32x4r r0, r1;
+        r0.x = o0[0] | (static_cast<uint32_t>(o0[1]) << 16);
+        r0.y = o0[2] | (static_cast<uint32_t>(o0[3]) << 16);
+        r0.z = o0[4] | (static_cast<uint32_t>(o0[5]) << 16);
+        r0.w = o0[6] | (static_cast<uint32_t>(o0[7]) << 16);
+        r1.x = o1[0] | (static_cast<uint32_t>(o1[1]) << 16);
+        r1.y = o1[2] | (static_cast<uint32_t>(o1[3]) << 16);
+        r1.z = o1[4] | (static_cast<uint32_t>(o1[5]) << 16);
+        r1.w = o1[6] | (static_cast<uint32_t>(o1[7]) << 16);
+        __builtin_nontemporal_store(r0, reinterpret_cast<u32x4r*>(out + base + p));
+        __builtin_nontemporal_store(r1, reinterpret_cast<u32x4r*>(out + base + p + half));
     } else {
         out[base + p] = o0[0];
         out[base + p + half] = o1[0];
@@ -588,16 +613,17 @@ hipError_t launch_rope_half_f32(hipStream_t stream, const float* x, const float*
                                 const float* sine, float* out, uint32_t tokens, uint32_t heads,
                                 uint32_t head_dim, uint32_t rope_stride) {
     const uint32_t half = head_dim / 2;
-    const bool vec = (half % 4) == 0 && aligned(x, 16) && aligned(out, 16);
+    const bool vec = (half % 4) == 0 && (rope_stride % 4) == 0 && aligned(x, 16) && aligned(out, 16) &&
+                     aligned(cosine, 16) && aligned(sine, 16);
     const uint32_t P = vec ? 4 : 1;
     const uint64_t threads = static_cast<uint64_t>(tokens) * heads * (half / P);
     const dim3 grid(static_cast<uint32_t>((threads + 255) / 256));
     if (vec)
-        hipLaunchKernelGGL((rope_half_f32_kernel<4>), grid, dim3(256), 0, stream, x, cosine, sine, out,
-                           tokens, heads, head_dim, rope_stride);
+        hipLaunchKernelGGL((rope_half_f32_kernel<4>), grid, dim3(256), 0, stream, x, cosine, sine, out, tokens,
+                           heads, head_dim, rope_stride);
     else
-        hipLaunchKernelGGL((rope_half_f32_kernel<1>), grid, dim3(256), 0, stream, x, cosine, sine, out,
-                           tokens, heads, head_dim, rope_stride);
+        hipLaunchKernelGGL((rope_half_f32_kernel<1>), grid, dim3(256), 0, stream, x, cosine, sine, out, tokens,
+                           heads, head_dim, rope_stride);
     return hipGetLastError();
 }
 
@@ -605,16 +631,17 @@ hipError_t launch_rope_half_f16(hipStream_t stream, const uint16_t* x, const flo
                                 const float* sine, uint16_t* out, uint32_t tokens, uint32_t heads,
                                 uint32_t head_dim, uint32_t rope_stride) {
     const uint32_t half = head_dim / 2;
-    const bool vec = (half % 4) == 0 && aligned(x, 8) && aligned(out, 8);
-    const uint32_t P = vec ? 4 : 1;
+    const bool vec = (half % 8) == 0 && (rope_stride % 4) == 0 && aligned(x, 16) && aligned(out, 16) &&
+                     aligned(cosine, 16) && aligned(sine, 16);
+    const uint32_t P = vec ? 8 : 1;
     const uint64_t threads = static_cast<uint64_t>(tokens) * heads * (half / P);
     const dim3 grid(static_cast<uint32_t>((threads + 255) / 256));
     if (vec)
-        hipLaunchKernelGGL((rope_half_f16_kernel<4>), grid, dim3(256), 0, stream, x, cosine, sine, out,
-                           tokens, heads, head_dim, rope_stride);
+        hipLaunchKernelGGL((rope_half_f16_kernel<8>), grid, dim3(256), 0, stream, x, cosine, sine, out, tokens,
+                           heads, head_dim, rope_stride);
     else
-        hipLaunchKernelGGL((rope_half_f16_kernel<1>), grid, dim3(256), 0, stream, x, cosine, sine, out,
-                           tokens, heads, head_dim, rope_stride);
+        hipLaunchKernelGGL((rope_half_f16_kernel<1>), grid, dim3(256), 0, stream, x, cosine, sine, out, tokens,
+                           heads, head_dim, rope_stride);
     return hipGetLastError();
 }
 

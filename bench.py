@@ -125,6 +125,61 @@ class Ops:
                 rt.free(b)
 
 
+class ConfigOps(Ops):
+    """Per-op timing at the other op configurations (separate lines, not the headline):
+    c1 = BASELINE configs[0] (SmolLM2-135M-shaped FP32 ops, T=128),
+    c2 = BASELINE configs[1] (SmolLM2-1.7B-shaped FP16 storage, T=2048)."""
+
+    def __init__(self, wl, rope_tables, cfg):
+        r = wl.rng(2025)
+        h16 = lambda a: a.astype(np.float16).view(np.uint16)
+        self.host, self.table = {}, {}
+        if cfg == "c2":
+            S = wl.LlamaPrefillShape()
+            T, H, NH, D, F = S.tokens, S.hidden, S.heads, S.head_dim, S.ffn
+            cos, sin = rope_tables(np.arange(T, dtype=np.uint32), D, S.theta)
+            self.tokens = T
+            self.host = {"x": h16(wl.normal(r, T * H)), "res": h16(wl.normal(r, T * H)),
+                         "w": h16(wl.normal(r, H, 1.0, 0.1)), "q": h16(wl.normal(r, T * NH * D)),
+                         "k": h16(wl.normal(r, T * NH * D)), "cos": cos, "sin": sin,
+                         "gate": h16(wl.normal(r, T * F)), "up": h16(wl.normal(r, T * F))}
+            self.table = {
+                "add_rms_norm_f16": (["x", "res", "w"], {"rs": T * H // 2, "y": T * H // 2}, 4 * T * H * 2 + H * 2,
+                                     lambda rt, s: rt.add_rms_norm_f16(s["x"], s["res"], s["w"], s["rs"], s["y"], T,
+                                                                       H, S.eps)),
+                "rope_half_f16_qk": (["q", "k", "cos", "sin"], {"qo": T * NH * D // 2, "ko": T * NH * D // 2},
+                                     4 * T * NH * D * 2 + 2 * T * (D // 2) * 4,
+                                     lambda rt, s: (rt.rope_half_f16(s["q"], s["cos"], s["sin"], s["qo"], T, NH, D,
+                                                                     D // 2),
+                                                    rt.rope_half_f16(s["k"], s["cos"], s["sin"], s["ko"], T, NH, D,
+                                                                     D // 2))),
+                "swiglu_f16": (["gate", "up"], {"o": T * F // 2}, 3 * T * F * 2,
+                               lambda rt, s: rt.swiglu_f16(s["gate"], s["up"], s["o"], T * F)),
+            }
+        else:
+            S = wl.SmolShape()
+            T, H, QH, KH, D, F, V = S.tokens, S.hidden, S.q_heads, S.kv_heads, S.head_dim, S.ffn, S.vocab
+            cos, sin = rope_tables(np.arange(T, dtype=np.uint32), D, S.theta)
+            self.tokens = T
+            self.host = {"x": wl.normal(r, T * H), "w": wl.normal(r, H, 1.0, 0.1), "q": wl.normal(r, T * QH * D),
+                         "k": wl.normal(r, T * KH * D), "cos": cos, "sin": sin, "gate": wl.normal(r, T * F),
+                         "up": wl.normal(r, T * F), "table": wl.normal(wl.rng(0), V * H, 0.0, 0.02),
+                         "ids": wl.token_ids(wl.rng(0), T, V)}
+            self.table = {
+                "rms_norm": (["x", "w"], {"y": T * H}, 2 * T * H * 4 + H * 4,
+                             lambda rt, s: rt.rms_norm(s["x"], s["w"], s["y"], T, H, S.eps)),
+                "rope_half_qk": (["q", "k", "cos", "sin"], {"qo": T * QH * D, "ko": T * KH * D},
+                                 2 * T * (QH + KH) * D * 4 + 2 * T * (D // 2) * 4,
+                                 lambda rt, s: (rt.rope_half(s["q"], s["cos"], s["sin"], s["qo"], T, QH, D, D // 2),
+                                                rt.rope_half(s["k"], s["cos"], s["sin"], s["ko"], T, KH, D, D // 2))),
+                "swiglu": (["gate", "up"], {"o": T * F}, 3 * T * F * 4,
+                           lambda rt, s: rt.swiglu(s["gate"], s["up"], s["o"], T * F)),
+                "embed_f32": (["table", "ids"], {"e": T * H}, T * H * 4 + T * 4 + T * H * 4,
+                              lambda rt, s: rt.embed_f32(s["table"], s["ids"], s["e"], V, H, T)),
+            }
+
+
+
 def time_launches(rt, launch, sets, iters):
     for i in range(3):
         launch(rt, sets[i % len(sets)])
@@ -248,6 +303,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma-separated op subset: per-op timing only (profiling)")
     ap.add_argument("--copy-mib", type=int, default=0, help="also time a device-to-device copy of this size")
+    ap.add_argument("--config", choices=["c3c4", "c1", "c2"], default="c3c4",
+                    help="c1 / c2: per-op lines for BASELINE configs[0] / configs[1] instead of the headline")
     ap.add_argument("--decode", action="store_true",
                     help="BASELINE configs[4] batched decode (per-layer latency, eager and HIP graph) instead")
     args = ap.parse_args()
@@ -263,6 +320,24 @@ def main():
     rt = HipRuntime(0, ATLAS_REDUCTION_WIDE if args.reduction == "wide" else ATLAS_REDUCTION_SEQUENTIAL)
     if args.decode:
         print(json.dumps(decode_bench(rt, min(args.steps, 50), min(args.warmup, 5))))
+        rt.close()
+        return
+    if args.config != "c3c4":
+        from atlas_amd import rope_tables_llama
+
+        cops = ConfigOps(wl, rope_tables_llama, args.config)
+        per_op = {}
+        for name, (_, _, nbytes, launch) in cops.table.items():
+            nsets = min(64, max(4, math.ceil(ROTATION_BYTES / cops.set_bytes(name))))
+            log(f"timing {args.config} {name} ({nsets} rotating sets)")
+            sets = cops.build_sets(rt, [name], nsets)
+            ms = time_launches(rt, launch, sets, args.op_iters)
+            cops.free_sets(rt, sets)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            per_op[name] = {"us": round(ms * 1e3, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
+                            "frac": round(gbs / HBM_PEAK_GBS, 4),
+                            "tokens_per_s": round(cops.tokens / (ms * 1e-3), 1), "rotating_sets": nsets}
+        print(json.dumps({"config": args.config, "per_op": per_op}))
         rt.close()
         return
     ops = Ops(wl, rope_tables_gemma4)

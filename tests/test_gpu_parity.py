@@ -392,3 +392,37 @@ def test_rms_exact_fold_adversarial_rows(rt, ora, hidden, mode):
     inp["x"] = _adversarial_rows(rows, hidden, 5000 + hidden)
     say(f"rms exact fold adversarial {mode} rows={rows} hidden={hidden}")
     _assert_bits_nan_equal(f"rms_{mode}", cases.rms_gpu(rt, inp, m), cases.rms_oracle(ora, inp, m))
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 8), (33, 576), (2050, 2048), (7, 4096), (19, 2056), (5, 1000),
+                                         (3, 8200), (4100, 64)])
+def test_f16_norms_shapes(rt, ora, rows, hidden):
+    """FP16-storage RMSNorm and add+RMSNorm: register engine (hidden % 8 == 0,
+    <= 4096, both row-per-wave counts) and the LDS fallback."""
+    inp, m = cases.f16_norm_case(rows, hidden, 1e-5, 7000 + rows + hidden)
+    say(f"f16 norms rows={rows} hidden={hidden}")
+    assert_bits("f16 norms", cases.f16_norm_gpu(rt, inp, m), cases.f16_norm_oracle(ora, inp, m))
+
+
+def test_f16_norm_aliasing(rt, ora):
+    """residual_out == input (the pre-norm add writes the residual stream in place)."""
+    rows, h = 64, 2048
+    inp, m = cases.f16_norm_case(rows, h, 1e-5, 7777)
+    rs_exp, y_exp = ora.add_rms_norm_f16(inp["x"], inp["res"], inp["w"], rows, h, 1e-5)
+    say("f16 add+norm in place")
+    x, res, w = rt.upload(inp["x"]), rt.upload(inp["res"]), rt.upload(inp["w"])
+    y = rt.empty(rows * h, np.uint16)
+    rt.add_rms_norm_f16(x, res, w, x, y, rows, h, 1e-5)
+    rt.sync()
+    assert_bits("f16 in place", [x.download(rows * h), y.download(rows * h)], [rs_exp, y_exp])
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("tokens,heads,head_dim", [(2048, 32, 64), (37, 3, 128), (5, 2, 96), (9, 4, 6), (3, 1, 256),
+                                                   (11, 5, 24)])
+def test_rope_half_shapes(rt, ora, f16, tokens, heads, head_dim):
+    """Half-split RoPE: 128-bit paths (half % 4 / % 8) and the scalar path."""
+    inp, m = cases.rope_half_case(tokens, heads, head_dim, 130000.0, 8000 + tokens + head_dim, f16)
+    say(f"rope_half f16={f16} tokens={tokens} heads={heads} head_dim={head_dim}")
+    tables = rope_tables_llama(inp["pos"], head_dim, 130000.0)
+    assert_bits("rope_half", cases.rope_half_gpu(rt, inp, m, tables), cases.rope_half_oracle(ora, inp, m))
