@@ -37,15 +37,21 @@ __device__ __forceinline__ float pow2i(int k) {  // 2^k, k in [-126, 127]
 // (fma, floor, exact power-of-two multiply), so the CPU oracle's restatement
 // with C99 fmaf gives the same bits; the result is faithfully rounded
 // (< 1 ulp against float64 exp over the finite range).
-__device__ __forceinline__ float exp_f32(float x) {
-    if (x != x) return x;
-    if (x > 89.0f) return __builtin_inff();
-    if (x < -104.0f) return 0.0f;
+//
+// The kernels stream HBM, so control flow is kept out of the math: the
+// special ranges are selected after the fact instead of branched on (a
+// branch per element costs an exec-mask round trip per wave and measured
+// ~10 % of GeGLU's time).  exp_small_f32 is the form for arguments known to
+// lie in (-87, 87), where no special range applies.
+__device__ __forceinline__ float exp_reduced(float x, int& n) {
     const float log2e = 1.44269502162933349609375f;
     const float ln2_hi = 0.693359375f;
     const float ln2_lo = -2.12194440e-4f;
-    const float fn = floorf(__builtin_fmaf(x, log2e, 0.5f));
-    const int n = static_cast<int>(fn);
+    // floor(x*log2e + 1/2), clamped so the integer conversion is defined for
+    // every input (NaN and |x| > 138 leave the clamp's range; their results
+    // are selected away or stay NaN through r)
+    const float fn = fminf(fmaxf(floorf(__builtin_fmaf(x, log2e, 0.5f)), -200.0f), 200.0f);
+    n = static_cast<int>(fn);
     const float r = __builtin_fmaf(-fn, ln2_lo, __builtin_fmaf(-fn, ln2_hi, x));
     float p = 1.0f / 5040.0f;
     p = __builtin_fmaf(p, r, 1.0f / 720.0f);
@@ -55,29 +61,74 @@ __device__ __forceinline__ float exp_f32(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    if (n > 127) return (p * pow2i(127)) * pow2i(n - 127);
-    if (n < -126) return (p * pow2i(n + 100)) * pow2i(-100);
-    return p * pow2i(n);
+    return p;
+}
+
+// e^x for |x| < 87 (n in [-126, 127]): one exact scale by 2^n.  Outside that
+// domain the value is meaningless and must be selected away by the caller.
+__device__ __forceinline__ float exp_small_f32(float x) {
+    int n;
+    const float p = exp_reduced(x, n);
+    return p * __uint_as_float(static_cast<uint32_t>(n + 127) << 23);
+}
+
+// e^x over the whole binary32 range.  Outside n in [-126, 127] the scale is
+// split in two steps, (p * 2^127) * 2^(n-127) or (p * 2^(n+100)) * 2^-100,
+// so the only rounding is the final (possibly subnormal) product; in range
+// the second factor is 1.0.  NaN returns x, x > 89 returns +inf and
+// x < -104 returns +0.
+__device__ __forceinline__ float exp_f32(float x) {
+    int n;
+    const float p = exp_reduced(x, n);  // n in [-200, 200]
+    const int s1 = n > 127 ? 127 : (n < -126 ? n + 100 : n);
+    const int s2 = n > 127 ? n - 127 : (n < -126 ? -100 : 0);
+    const float y = (p * pow2i(s1)) * pow2i(s2);
+    const float big = x > 89.0f ? __builtin_inff() : y;
+    const float out = x < -104.0f ? 0.0f : big;
+    return x != x ? x : out;
 }
 
 // tanh through its exponential identity with saturation at |x| >= 10
 // (Atlas atlas_tanh_f32, crates/atlas-metal/src/kernels.metal:742-750).
+// Inside (-10, 10), 2v is inside (-20, 20), where exp_small_f32 is exact
+// to exp_f32; outside, the quotient is computed and discarded.  NaN
+// propagates through the quotient.
 __device__ __forceinline__ float tanh_f32(float v) {
-    if (v >= 10.0f) return 1.0f;
-    if (v <= -10.0f) return -1.0f;
-    float e = exp_f32(2.0f * v);
-    return fdiv_rn(e - 1.0f, e + 1.0f);
+    const float e = exp_small_f32(2.0f * v);
+    const float q = fdiv_rn(e - 1.0f, e + 1.0f);
+    return v >= 10.0f ? 1.0f : (v <= -10.0f ? -1.0f : q);
 }
 
 // x / (1 + e^-x)   (kernels.metal:27-36)
 __device__ __forceinline__ float silu_f32(float x) { return fdiv_rn(x, 1.0f + exp_f32(-x)); }
 
+// silu_f32 for |x| < 87, where exp_small_f32(-x) == exp_f32(-x).
+__device__ __forceinline__ float silu_small_f32(float x) { return fdiv_rn(x, 1.0f + exp_small_f32(-x)); }
+
+// SiLU of N values held by each lane.  When every value of the wavefront
+// lies in (-87, 87) -- all ordinary activations -- the straight-line
+// in-range form runs; otherwise (huge inputs, inf, NaN) the full-range form
+// runs for the whole wavefront.  One wave-uniform branch, same bits.
+template <int N>
+__device__ __forceinline__ void silu_lanes(float (&v)[N]) {
+    bool small = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) small = small && __builtin_fabsf(v[i]) < 87.0f;
+    if (__builtin_amdgcn_ballot_w64(!small) == 0) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = silu_small_f32(v[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = silu_f32(v[i]);
+    }
+}
+
 // tanh-GELU with the overflow guard (kernels.metal:752-767):
 // a = c0*(x + ((c1*x)*x)*x); inf(a) -> (a > 0 ? x : 0); else (0.5*x)*(1 + tanh(a)).
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
-    float argument = 0.7978845608f * (x + 0.044715f * x * x * x);
-    if (__builtin_isinf(argument)) return argument > 0.0f ? x : 0.0f;
-    return 0.5f * x * (1.0f + tanh_f32(argument));
+    const float argument = 0.7978845608f * (x + 0.044715f * x * x * x);
+    const float g = 0.5f * x * (1.0f + tanh_f32(argument));
+    return __builtin_isinf(argument) ? (argument > 0.0f ? x : 0.0f) : g;
 }
 
 // 1 / sqrt(mean + eps) with the CPU operators' two roundings

@@ -43,10 +43,17 @@ __global__ __launch_bounds__(256) void elementwise_vec_kernel(const float* a, co
         f32x4 vb = f32x4{0.f, 0.f, 0.f, 0.f};
         if (binary(OP)) vb = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(b) + i);
         f32x4 r;
-        r.x = elt<OP>(va.x, vb.x, scalar);
-        r.y = elt<OP>(va.y, vb.y, scalar);
-        r.z = elt<OP>(va.z, vb.z, scalar);
-        r.w = elt<OP>(va.w, vb.w, scalar);
+        if (OP == kEltSilu || OP == kEltSwiglu) {
+            float g[4] = {va.x, va.y, va.z, va.w};
+            silu_lanes(g);
+            r = OP == kEltSwiglu ? f32x4{g[0] * vb.x, g[1] * vb.y, g[2] * vb.z, g[3] * vb.w}
+                                 : f32x4{g[0], g[1], g[2], g[3]};
+        } else {
+            r.x = elt<OP>(va.x, vb.x, scalar);
+            r.y = elt<OP>(va.y, vb.y, scalar);
+            r.z = elt<OP>(va.z, vb.z, scalar);
+            r.w = elt<OP>(va.w, vb.w, scalar);
+        }
         __builtin_nontemporal_store(r, reinterpret_cast<f32x4*>(out) + i);
     }
 }
@@ -63,9 +70,11 @@ __global__ __launch_bounds__(256) void elementwise_scalar_kernel(const float* a,
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Eight f16 values per operand per thread (one 128-bit nontemporal access).
-__device__ __forceinline__ uint32_t swiglu_f16_pair(uint32_t g, uint32_t u) {
-    const uint32_t lo = f2h(silu_f32(h2f(static_cast<uint16_t>(g))) * h2f(static_cast<uint16_t>(u)));
-    const uint32_t hi = f2h(silu_f32(h2f(static_cast<uint16_t>(g >> 16))) * h2f(static_cast<uint16_t>(u >> 16)));
+// Gates are widened exactly to f32; a wavefront holding a gate of magnitude
+// >= 87 (or inf/NaN) takes silu_lanes' full-range form.
+__device__ __forceinline__ uint32_t mul_pack_f16(float g_lo, float g_hi, uint32_t u) {
+    const uint32_t lo = f2h(g_lo * h2f(static_cast<uint16_t>(u)));
+    const uint32_t hi = f2h(g_hi * h2f(static_cast<uint16_t>(u >> 16)));
     return lo | (hi << 16);
 }
 
@@ -75,8 +84,13 @@ __global__ __launch_bounds__(256) void swiglu_f16_kernel(const uint16_t* gate, c
     for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n8; i += stride) {
         const u32x4 g = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gate) + i);
         const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(up) + i);
-        const u32x4 r{swiglu_f16_pair(g.x, u.x), swiglu_f16_pair(g.y, u.y), swiglu_f16_pair(g.z, u.z),
-                      swiglu_f16_pair(g.w, u.w)};
+        float a[8] = {h2f(static_cast<uint16_t>(g.x)), h2f(static_cast<uint16_t>(g.x >> 16)),
+                      h2f(static_cast<uint16_t>(g.y)), h2f(static_cast<uint16_t>(g.y >> 16)),
+                      h2f(static_cast<uint16_t>(g.z)), h2f(static_cast<uint16_t>(g.z >> 16)),
+                      h2f(static_cast<uint16_t>(g.w)), h2f(static_cast<uint16_t>(g.w >> 16))};
+        silu_lanes(a);
+        const u32x4 r{mul_pack_f16(a[0], a[1], u.x), mul_pack_f16(a[2], a[3], u.y), mul_pack_f16(a[4], a[5], u.z),
+                      mul_pack_f16(a[6], a[7], u.w)};
         __builtin_nontemporal_store(r, reinterpret_cast<u32x4*>(out) + i);
     }
 }
