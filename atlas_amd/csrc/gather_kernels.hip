@@ -66,21 +66,42 @@ __device__ __forceinline__ void q6_k_decode4(const uint8_t* row, uint32_t col, f
     }
 }
 
+// Copy `units` elements of type U from global `src` to LDS `dst` with
+// threads [0, nthreads).  Each pass issues K loads per thread before the
+// first LDS write, so a row costs one HBM round trip per pass instead of one
+// per load (a plain copy loop waits on every load).  K is sized per call
+// site to the row: extra guarded slots cost registers and branches.
+template <int K, typename U>
+__device__ __forceinline__ void stage_units(uint8_t* dst, const uint8_t* src, uint32_t units, uint32_t tid,
+                                            uint32_t nthreads) {
+    for (uint32_t base = 0; base < units; base += K * nthreads) {
+        U v[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const uint32_t i = base + tid + k * nthreads;
+            if (i < units) v[k] = reinterpret_cast<const U*>(src)[i];
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const uint32_t i = base + tid + k * nthreads;
+            if (i < units) reinterpret_cast<U*>(dst)[i] = v[k];
+        }
+    }
+}
+
 // Copy `bytes` (even) from global `src` to LDS `dst` with the widest
-// coalesced access the source alignment permits; threads [0, nthreads).
+// access the source alignment permits; threads [0, nthreads).  K16 / K4 /
+// K2: loads in flight per thread for 16-, 4- and 2-byte accesses.
+template <int K16, int K4, int K2>
 __device__ __forceinline__ void stage_row(uint8_t* dst, const uint8_t* src, uint32_t bytes,
                                           uint32_t tid, uint32_t nthreads) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(src);
-    if ((a & 15) == 0 && (bytes & 15) == 0) {
-        for (uint32_t i = tid; i < bytes / 16; i += nthreads)
-            reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
-    } else if ((a & 3) == 0 && (bytes & 3) == 0) {
-        for (uint32_t i = tid; i < bytes / 4; i += nthreads)
-            reinterpret_cast<uint32_t*>(dst)[i] = reinterpret_cast<const uint32_t*>(src)[i];
-    } else {
-        for (uint32_t i = tid; i < bytes / 2; i += nthreads)
-            reinterpret_cast<uint16_t*>(dst)[i] = reinterpret_cast<const uint16_t*>(src)[i];
-    }
+    if ((a & 15) == 0 && (bytes & 15) == 0)
+        stage_units<K16, uint4>(dst, src, bytes / 16, tid, nthreads);
+    else if ((a & 3) == 0 && (bytes & 3) == 0)
+        stage_units<K4, uint32_t>(dst, src, bytes / 4, tid, nthreads);
+    else
+        stage_units<K2, uint16_t>(dst, src, bytes / 2, tid, nthreads);
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -131,7 +152,7 @@ __global__ __launch_bounds__(64) void embed_quant_kernel(const uint8_t* __restri
     // the reference kernels leave rows with id >= vocab untouched
     if (id >= vocab) return;
     const uint32_t row_bytes = Q6 ? (hidden / 256) * 210 : (hidden / 32) * 18;
-    stage_row(row, table + static_cast<size_t>(id) * row_bytes, row_bytes, lane, kWave);
+    stage_row<1, 5, 8>(row, table + static_cast<size_t>(id) * row_bytes, row_bytes, lane, kWave);
     __syncthreads();
     float* dst = out + static_cast<size_t>(t) * hidden;
     for (uint32_t c = lane * 4; c < hidden; c += 4 * kWave) {
@@ -168,7 +189,7 @@ __global__ __launch_bounds__(256) void ple_quant_kernel(const uint8_t* __restric
         p[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(projection + base) + c4);
     }
     const uint32_t row_bytes = Q6 ? (row_elems / 256) * 210 : (row_elems / 32) * 18;
-    stage_row(row, table + static_cast<size_t>(id) * row_bytes, row_bytes, threadIdx.x, blockDim.x);
+    stage_row<1, 4, 8>(row, table + static_cast<size_t>(id) * row_bytes, row_bytes, threadIdx.x, blockDim.x);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
