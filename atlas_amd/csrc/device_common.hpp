@@ -194,4 +194,109 @@ __device__ __forceinline__ float fold_lds_chunk(const f32x4* p, uint32_t n4, flo
     return s;
 }
 
+// ---------------------------------------------------------------------------
+// Exact wave-parallel continuation of a sequential f32 fold.
+//
+// The CPU operators fold x_i*x_i left to right in f32, and the cancelling
+// epilogues make that order observable, so the sum must come out bit-exact.
+// A dependent add chain costs ~8 cycles per add; this computes the same
+// bits with the chunk spread across the wavefront:
+//
+//  * The running sum s is a non-negative float in a binade [2^E, 2^(E+1)),
+//    so it is an integer k of ulps u = 2^(E-23).  While the sum stays in the
+//    binade, s + a rounds to s + round(a/u)*u: every addend contributes an
+//    integer number of ulps that does not depend on s -- except at an exact
+//    tie (a/u = m + 1/2), where round-half-even looks at the parity of k.
+//  * So each lane converts its S addends to ulps (exact: a scale by a power
+//    of two, rint, and an exact sum of at most S integers below 2^21) and
+//    the wavefront takes an inclusive prefix sum of the per-lane counts
+//    (DPP row shifts and row broadcasts, u32).
+//  * In integer form, adding P ulps to s within the binade is adding P to
+//    its bit pattern.  The first lane whose prefix reaches the next power of
+//    two (K = 2^24 - k ulps away), or that holds a tie or an out-of-range
+//    addend, is an event: the lanes before it are applied as one integer add,
+//    the event lane's S values are folded one by one in f32, and the scan is
+//    reused (same binade) or recomputed (new binade).
+//  * Sums outside [2^-100, 2^125), inf and NaN fold lane by lane in f32.
+//
+// Every step either is the sequential fold's own f32 add or provably equals
+// it, so the result is the sequential fold's bit pattern.  The wave must be
+// fully active (64 lanes) and all addends >= +0 or NaN (squares).
+//
+// v: lane l's S consecutive addends [S*l, S*l + S) of the chunk;
+// sb: bit pattern of the running sum before the chunk (wave-uniform).
+// Returns the bit pattern after the chunk (wave-uniform).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, uint32_t lane) {
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), static_cast<int>(lane)));
+}
+__device__ __forceinline__ float readlane_f32(float v, uint32_t lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), static_cast<int>(lane)));
+}
+
+// Inclusive prefix sum over the 64 lanes (u32, wrapping).  Row shifts by 1,
+// 2, 4, 8 scan each row of 16 lanes (zero fill); row_bcast:15 adds row 0's
+// total to row 1 and row 2's to row 3; row_bcast:31 adds rows 0-1's total
+// to rows 2 and 3.
+__device__ __forceinline__ uint32_t wave_inclusive_scan_u32(uint32_t v) {
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xf, 0xf, true));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xf, 0xf, true));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xf, 0xf, true));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xf, 0xf, true));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xa, 0xf, false));
+    v += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, false));
+    return v;
+}
+
+template <int S>
+__device__ __forceinline__ uint32_t fold_chunk_exact(const float (&v)[S], uint32_t sb) {
+    const uint32_t lane = __lane_id();
+    uint32_t l0 = 0;
+    while (l0 < 64) {
+        const uint32_t ex = sb >> 23;  // biased exponent (NaN/inf: >= 255)
+        if (ex < 27 || ex > 251) {
+            float s = __uint_as_float(sb);
+#pragma unroll
+            for (int i = 0; i < S; ++i) s = s + readlane_f32(v[i], l0);
+            sb = __float_as_uint(s);
+            ++l0;
+            continue;
+        }
+        const float inv_ulp = __uint_as_float((277u - ex) << 23);  // 2^(23-E)
+        float ulps = 0.0f, dev = 0.0f;
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            const float q = v[i] * inv_ulp;
+            const float m = __builtin_rintf(q);
+            dev = fmaxf(dev, __builtin_fabsf(q - m));
+            ulps = ulps + m;
+        }
+        const bool bad = !(ulps < 2097152.0f) || dev == 0.5f;  // out of range, NaN/inf, or a tie
+        const uint32_t inc = bad ? 0u : static_cast<uint32_t>(ulps);
+        const uint32_t incl = wave_inclusive_scan_u32(inc);
+        const uint64_t badmask = __builtin_amdgcn_ballot_w64(bad);
+        uint32_t base = l0 ? readlane_u32(incl, l0 - 1) : 0u;
+        for (;;) {
+            const uint32_t room = 0x800000u - (sb & 0x7fffffu);  // ulps to the next power of two
+            const uint64_t ev = (__builtin_amdgcn_ballot_w64(incl - base >= room) | badmask) & (~0ull << l0);
+            if (ev == 0) {
+                sb += readlane_u32(incl, 63) - base;
+                l0 = 64;
+                break;
+            }
+            const uint32_t lc = static_cast<uint32_t>(__builtin_ctzll(ev));
+            const uint32_t incl_lc = readlane_u32(incl, lc);
+            sb += incl_lc - readlane_u32(inc, lc) - base;  // lanes [l0, lc): same binade, exact
+            float s = __uint_as_float(sb);
+#pragma unroll
+            for (int i = 0; i < S; ++i) s = s + readlane_f32(v[i], lc);
+            sb = __float_as_uint(s);
+            base = incl_lc;
+            l0 = lc + 1;
+            if (l0 >= 64 || (sb >> 23) != ex) break;
+        }
+    }
+    return sb;
+}
+
 }  // namespace atlas

@@ -212,11 +212,14 @@ __global__ __launch_bounds__(256) void rms_wide_kernel(NormArgs a) {
 //   1. every load of the wave is issued up front (the rows, the epilogue
 //      operand -- residual or state -- and the weights), streamed with
 //      nontemporal loads;
-//   2. as chunk j lands, its squares go to LDS and lane r folds row r's
-//      chunk j in index order while later chunks are still in flight.  The
-//      f32 fold is a dependent add chain (~8 cycles per add on gfx950, ~12K
-//      cycles for 1536 values), so it must overlap the loads rather than sit
-//      between the load and store phases;
+//   2. as chunk j lands, it is folded while later chunks are still in
+//      flight.  The f32 fold is a dependent add chain (~8 cycles per add on
+//      gfx950, ~12K cycles for 1536 values), so it must overlap the loads
+//      rather than sit between the load and store phases.  Chunk 0 (256
+//      values) always goes to LDS and lane r folds row r in index order.
+//      Later chunks either do the same (PAR = false) or go through
+//      fold_chunk_exact, the exact wave-parallel continuation of the fold
+//      (PAR = true): same bits, a fraction of the latency, more VALU work;
 //   3. lane r's inverse RMS is broadcast with readlane and every lane
 //      finishes its columns with nontemporal stores.
 // Each row is fully read before any of its outputs is written, so the
@@ -231,7 +234,7 @@ __device__ __forceinline__ void stg_nt(float* p, f32x4 v) {
 }
 
 
-template <int R, int J, int MODE>
+template <int R, int J, int MODE, bool PAR>
 __global__ __launch_bounds__(64) void rms_reg_kernel(NormArgs a) {
     // Squares of R rows, (hidden/4 + 1) float4 per row.  The load phase is
     // straight-line code (rows past the end and columns past the row width
@@ -265,6 +268,7 @@ __global__ __launch_bounds__(64) void rms_reg_kernel(NormArgs a) {
     for (int j = 0; j < J; ++j) w[j] = ldg(a.weight + 4 * min(lane + 64u * j, nv - 1));
 
     float s = 0.0f;  // lane r < nrows: running sum of squares of row r
+    uint32_t sb[R];  // PAR: running sums of squares (bit patterns, wave-uniform)
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const uint32_t creal = lane + 64u * j;
@@ -277,10 +281,28 @@ __global__ __launch_bounds__(64) void rms_reg_kernel(NormArgs a) {
                 v = f32x4{v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w};
                 x[r][j] = v;
             }
-            sq4[r * stride4 + c] = f32x4{v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w};
+            if (!PAR || j == 0) {
+                sq4[r * stride4 + c] = f32x4{v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w};
+            } else if (static_cast<uint32_t>(r) < nrows) {
+                // chunks after the first: exact wave-parallel fold (columns past
+                // the row width hold clamped duplicates and contribute +0)
+                const bool in_row = creal < nv;
+                const float sq[4] = {in_row ? v.x * v.x : 0.0f, in_row ? v.y * v.y : 0.0f,
+                                     in_row ? v.z * v.z : 0.0f, in_row ? v.w * v.w : 0.0f};
+                sb[r] = fold_chunk_exact<4>(sq, sb[r]);
+            }
         }
-        __syncthreads();
-        if (lane < nrows) s = fold_lds_chunk(sq4 + lane * stride4 + 64u * j, min(nv, 64u * (j + 1)) - 64u * j, s);
+        if (!PAR || j == 0) {
+            __syncthreads();
+            if (lane < nrows)
+                s = fold_lds_chunk(sq4 + lane * stride4 + 64u * j, min(nv, 64u * (j + 1)) - 64u * j, s);
+        }
+        if (PAR && j == 0) {
+            // the first chunk, where the sum crosses many binades and ties are
+            // frequent, folds in order; broadcast each row's partial sum
+#pragma unroll
+            for (int r = 0; r < R; ++r) sb[r] = readlane_u32(__float_as_uint(s), static_cast<uint32_t>(r));
+        }
     }
     if (MODE == kNormAddNorm) {  // stored residual stream r = x + residual
 #pragma unroll
@@ -299,7 +321,8 @@ __global__ __launch_bounds__(64) void rms_reg_kernel(NormArgs a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         if (static_cast<uint32_t>(r) >= nrows) break;
-        const float ir = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
+        const float ir = PAR ? inverse_rms(__uint_as_float(sb[r]), static_cast<float>(h), a.epsilon)
+                             : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const uint32_t c = lane + 64u * j;
@@ -333,45 +356,65 @@ bool lds_engine_forced() {
     return forced;
 }
 
-// Rows per wavefront for the register engine.
-int pick_reg_rows(uint32_t rows, int J, int mode) {
-    static const int forced = env_int("ATLAS_REG_ROWS", 0);
-    if (forced == 1 || forced == 2 || forced == 4) return forced;
-    // Measured on MI355X at [4096, 1536]: R = 2 (two wavefronts per SIMD)
-    // beats R = 4 (one wavefront per SIMD) by 20-30 % and R = 1 by 10-35 %.
-    (void)J;
-    (void)mode;
-    return rows >= 2048 ? 2 : 1;
+// Register-engine configuration: rows per wavefront and the fold of the
+// chunks after the first (exact wave-parallel, or in order from LDS).  Same
+// bits either way.  Measured on MI355X:
+//  * rows < 2048 (decode batches): one row per wavefront and the parallel
+//    fold -- the in-order chain is fully exposed there (C5 decode step at
+//    256 rows: 35.9 -> 30.3 us per layer);
+//  * rows >= 2048, plain RMSNorm: one row per wavefront, parallel fold
+//    ([4096, 1536]: 11.7 -> 10.6 us);
+//  * rows >= 2048 with an epilogue operand (residual, add-norm, add-scale):
+//    two rows per wavefront (two wavefronts per SIMD) and the in-order fold
+//    ([4096, 1536] residual: 16.0 us; one row and the parallel fold: 16.7).
+// ATLAS_REG_ROWS (1, 2, 4) and ATLAS_NORM_PAR_FOLD (0, 1) override for sweeps.
+struct RegConfig {
+    int rows;
+    bool par;
+};
+
+RegConfig pick_reg(uint32_t rows, int mode) {
+    static const int forced_rows = env_int("ATLAS_REG_ROWS", 0);
+    static const int forced_par = env_int("ATLAS_NORM_PAR_FOLD", -1);
+    RegConfig c{1, true};
+    if (rows >= 2048 && mode != kNormPlain) c = RegConfig{2, false};
+    if (forced_rows == 1 || forced_rows == 2 || forced_rows == 4) c.rows = forced_rows;
+    if (forced_par == 0 || forced_par == 1) c.par = forced_par == 1;
+    return c;
 }
 
 template <int R, int J, int MODE>
-hipError_t launch_reg_rj(hipStream_t s, const NormArgs& a) {
+hipError_t launch_reg_rj(hipStream_t s, const NormArgs& a, bool par) {
     const size_t lds = static_cast<size_t>(R) * (a.hidden / 4 + 1) * sizeof(f32x4);
-    hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE>), dim3((a.rows + R - 1) / R), dim3(kWave), lds, s, a);
+    if (par)
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true>), dim3((a.rows + R - 1) / R), dim3(kWave), lds, s, a);
+    else
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false>), dim3((a.rows + R - 1) / R), dim3(kWave), lds, s, a);
     return hipGetLastError();
 }
 
 template <int R, int MODE>
-hipError_t launch_reg_r(hipStream_t s, const NormArgs& a, int J) {
+hipError_t launch_reg_r(hipStream_t s, const NormArgs& a, int J, bool par) {
     switch (J) {
-        case 1: return launch_reg_rj<R, 1, MODE>(s, a);
-        case 2: return launch_reg_rj<R, 2, MODE>(s, a);
-        case 3: return launch_reg_rj<R, 3, MODE>(s, a);
-        case 4: return launch_reg_rj<R, 4, MODE>(s, a);
-        case 5: return launch_reg_rj<R, 5, MODE>(s, a);
-        case 6: return launch_reg_rj<R, 6, MODE>(s, a);
-        case 7: return launch_reg_rj<R, 7, MODE>(s, a);
-        default: return launch_reg_rj<R, 8, MODE>(s, a);
+        case 1: return launch_reg_rj<R, 1, MODE>(s, a, par);
+        case 2: return launch_reg_rj<R, 2, MODE>(s, a, par);
+        case 3: return launch_reg_rj<R, 3, MODE>(s, a, par);
+        case 4: return launch_reg_rj<R, 4, MODE>(s, a, par);
+        case 5: return launch_reg_rj<R, 5, MODE>(s, a, par);
+        case 6: return launch_reg_rj<R, 6, MODE>(s, a, par);
+        case 7: return launch_reg_rj<R, 7, MODE>(s, a, par);
+        default: return launch_reg_rj<R, 8, MODE>(s, a, par);
     }
 }
 
 template <int MODE>
 hipError_t launch_reg(hipStream_t s, const NormArgs& a) {
     const int J = static_cast<int>((a.hidden / 4 + 63) / 64);
-    switch (pick_reg_rows(a.rows, J, MODE)) {
-        case 4: return launch_reg_r<4, MODE>(s, a, J);
-        case 2: return launch_reg_r<2, MODE>(s, a, J);
-        default: return launch_reg_r<1, MODE>(s, a, J);
+    const RegConfig c = pick_reg(a.rows, MODE);
+    switch (c.rows) {
+        case 4: return launch_reg_r<4, MODE>(s, a, J, c.par);
+        case 2: return launch_reg_r<2, MODE>(s, a, J, c.par);
+        default: return launch_reg_r<1, MODE>(s, a, J, c.par);
     }
 }
 
@@ -573,7 +616,7 @@ __device__ __forceinline__ uint32_t pack16(float lo, float hi) {
     return static_cast<uint32_t>(f2h(lo)) | (static_cast<uint32_t>(f2h(hi)) << 16);
 }
 
-template <int R, int J, bool ADD>
+template <int R, int J, bool ADD, bool PAR>
 __global__ __launch_bounds__(64) void rms_reg_f16_kernel(const uint16_t* x, const uint16_t* residual,
                                                          const uint16_t* weight, uint16_t* residual_out,
                                                          uint16_t* out, uint32_t rows, uint32_t hidden,
@@ -603,9 +646,11 @@ __global__ __launch_bounds__(64) void rms_reg_f16_kernel(const uint16_t* x, cons
         wv[j] = *reinterpret_cast<const u32x4*>(weight + 8 * min(lane + 64u * j, n8 - 1));
 
     float s = 0.0f;
+    uint32_t sb[R];  // PAR: running sums of squares (bit patterns, wave-uniform)
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const uint32_t c = min(lane + 64u * j, n8 - 1);
+        const uint32_t creal = lane + 64u * j;
+        const uint32_t c = min(creal, n8 - 1);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             u32x4 v = xv[r][j];
@@ -619,14 +664,41 @@ __global__ __launch_bounds__(64) void rms_reg_f16_kernel(const uint16_t* x, cons
             }
             const float a0 = lo16(v.x), a1 = hi16(v.x), a2 = lo16(v.y), a3 = hi16(v.y);
             const float a4 = lo16(v.z), a5 = hi16(v.z), a6 = lo16(v.w), a7 = hi16(v.w);
-            sq4[r * stride4 + 2 * c] = f32x4{a0 * a0, a1 * a1, a2 * a2, a3 * a3};
-            sq4[r * stride4 + 2 * c + 1] = f32x4{a4 * a4, a5 * a5, a6 * a6, a7 * a7};
+            if (!PAR || j == 0) {
+                sq4[r * stride4 + 2 * c] = f32x4{a0 * a0, a1 * a1, a2 * a2, a3 * a3};
+                sq4[r * stride4 + 2 * c + 1] = f32x4{a4 * a4, a5 * a5, a6 * a6, a7 * a7};
+            } else if (static_cast<uint32_t>(r) < nrows) {
+                const bool in_row = creal < n8;
+                const float sq[8] = {in_row ? a0 * a0 : 0.0f, in_row ? a1 * a1 : 0.0f, in_row ? a2 * a2 : 0.0f,
+                                     in_row ? a3 * a3 : 0.0f, in_row ? a4 * a4 : 0.0f, in_row ? a5 * a5 : 0.0f,
+                                     in_row ? a6 * a6 : 0.0f, in_row ? a7 * a7 : 0.0f};
+                sb[r] = fold_chunk_exact<8>(sq, sb[r]);
+            }
         }
-        __syncthreads();
-        if (lane < nrows) {
-            const uint32_t begin = 128u * j, end = min(2 * n8, 128u * (j + 1));
-            const f32x4* row = sq4 + lane * stride4;
-            for (uint32_t k = begin; k < end; k += 64) s = fold_lds_chunk(row + k, min(64u, end - k), s);
+        if (!PAR || j == 0) {
+            __syncthreads();
+            if (lane < nrows) {
+                // PAR: only the first 256 values (lanes 0-31 of chunk 0) fold in order
+                const uint32_t begin = 128u * j, end = min(2 * n8, PAR ? 64u : 128u * (j + 1));
+                const f32x4* row = sq4 + lane * stride4;
+                for (uint32_t k = begin; k < end; k += 64) s = fold_lds_chunk(row + k, min(64u, end - k), s);
+            }
+        }
+        if (PAR && j == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                sb[r] = readlane_u32(__float_as_uint(s), static_cast<uint32_t>(r));
+                if (static_cast<uint32_t>(r) < nrows) {
+                    const u32x4 v = xv[r][0];
+                    const bool take = creal >= 32 && creal < n8;
+                    const float a0 = lo16(v.x), a1 = hi16(v.x), a2 = lo16(v.y), a3 = hi16(v.y);
+                    const float a4 = lo16(v.z), a5 = hi16(v.z), a6 = lo16(v.w), a7 = hi16(v.w);
+                    const float sq[8] = {take ? a0 * a0 : 0.0f, take ? a1 * a1 : 0.0f, take ? a2 * a2 : 0.0f,
+                                         take ? a3 * a3 : 0.0f, take ? a4 * a4 : 0.0f, take ? a5 * a5 : 0.0f,
+                                         take ? a6 * a6 : 0.0f, take ? a7 * a7 : 0.0f};
+                    sb[r] = fold_chunk_exact<8>(sq, sb[r]);
+                }
+            }
         }
     }
     if (ADD) {
@@ -646,7 +718,8 @@ __global__ __launch_bounds__(64) void rms_reg_f16_kernel(const uint16_t* x, cons
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         if (static_cast<uint32_t>(r) >= nrows) break;
-        const float ir = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
+        const float ir = PAR ? inverse_rms(__uint_as_float(sb[r]), static_cast<float>(hidden), epsilon)
+                             : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const uint32_t c = lane + 64u * j;
@@ -665,8 +738,15 @@ template <int R, int J, bool ADD>
 hipError_t launch_f16_reg_rj(hipStream_t s, const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
                              uint16_t* residual_out, uint16_t* out, uint32_t rows, uint32_t hidden, float eps) {
     const size_t lds = static_cast<size_t>(R) * (hidden / 4 + 1) * sizeof(f32x4);
-    hipLaunchKernelGGL((rms_reg_f16_kernel<R, J, ADD>), dim3((rows + R - 1) / R), dim3(kWave), lds, s, x, residual,
-                       weight, residual_out, out, rows, hidden, eps);
+    // FP16 rows ([2048, 2048] at C2) measured slower with the parallel fold
+    // (13.8 -> 16.7 us), so the in-order fold is the default here;
+    // ATLAS_NORM_PAR_FOLD=1 selects the parallel one (same bits).
+    if (env_int("ATLAS_NORM_PAR_FOLD", 0) == 1)
+        hipLaunchKernelGGL((rms_reg_f16_kernel<R, J, ADD, true>), dim3((rows + R - 1) / R), dim3(kWave), lds, s, x,
+                           residual, weight, residual_out, out, rows, hidden, eps);
+    else
+        hipLaunchKernelGGL((rms_reg_f16_kernel<R, J, ADD, false>), dim3((rows + R - 1) / R), dim3(kWave), lds, s, x,
+                           residual, weight, residual_out, out, rows, hidden, eps);
     return hipGetLastError();
 }
 
@@ -690,7 +770,10 @@ template <bool ADD>
 hipError_t launch_f16_reg(hipStream_t s, const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
                           uint16_t* residual_out, uint16_t* out, uint32_t rows, uint32_t hidden, float eps) {
     const int J = static_cast<int>((hidden / 8 + 63) / 64);
-    if (pick_reg_rows(rows, J, 0) == 2)
+    // two rows per wavefront from 2048 rows up (two wavefronts per SIMD);
+    // ATLAS_REG_ROWS (1, 2) overrides for sweeps
+    const int forced = env_int("ATLAS_REG_ROWS", 0);
+    if (forced == 2 || (forced != 1 && rows >= 2048))
         return launch_f16_reg_r<2, ADD>(s, J, x, residual, weight, residual_out, out, rows, hidden, eps);
     return launch_f16_reg_r<1, ADD>(s, J, x, residual, weight, residual_out, out, rows, hidden, eps);
 }

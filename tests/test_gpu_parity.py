@@ -384,10 +384,15 @@ def _assert_bits_nan_equal(name, got, exp):
                                  f"gpu={g[j]!r} oracle={e[j]!r}")
 
 
+@pytest.mark.parametrize("rows", [2048 + 48, 1024 + 16])
 @pytest.mark.parametrize("hidden", [1536, 2048, 576, 1024, 260])
 @pytest.mark.parametrize("mode", ["plain", "residual", "addnorm", "addscale"])
-def test_rms_exact_fold_adversarial_rows(rt, ora, hidden, mode):
-    rows = 2048 + 48   # R = 2 path (and its ragged tail), every row kind many times
+def test_rms_exact_fold_adversarial_rows(rt, ora, rows, hidden, mode):
+    """Both folds of the register engine against the oracle's sequential sum on
+    rows built to break a reordered or wave-parallel fold.  Below 2048 rows every
+    mode uses one row per wavefront and the exact wave-parallel fold; from 2048
+    rows up, plain RMSNorm keeps the parallel fold and the epilogue modes fold in
+    order with two rows per wavefront (and a ragged tail)."""
     inp, m = cases.rms_case(rows, hidden, 1e-6, 4000 + hidden, mode)
     inp["x"] = _adversarial_rows(rows, hidden, 5000 + hidden)
     say(f"rms exact fold adversarial {mode} rows={rows} hidden={hidden}")
