@@ -633,6 +633,63 @@ static int ple(atlas_hip_ctx* ctx, int q6, const uint8_t* table, const uint32_t*
                     q6 ? "ple_q6_k" : "ple_q4_0");
 }
 
+static int q4_matvec(atlas_hip_ctx* ctx, const float* input, const float* rms_weight, float epsilon,
+                     uint32_t input_width, uint32_t segments, const uint8_t* const* weights, float* const* outputs,
+                     const uint32_t* widths, const char* op) {
+    int rc = enter(ctx);
+    if (rc) return rc;
+    if (!input) return invalid(ctx, "matvec input is null");
+    if (input_width == 0 || input_width % 32 != 0 || input_width > atlas::q4_0_matvec_max_input())
+        return invalid(ctx, "matvec input_width must be a positive multiple of 32, at most 4096");
+    if (!aligned16(input) || (rms_weight && !aligned16(rms_weight)))
+        return invalid(ctx, "matvec input and rms_weight must be 16-byte aligned");
+    if (rms_weight && !finite_positive(epsilon)) return invalid(ctx, "epsilon must be finite and positive");
+    atlas::MatvecArgs a{};
+    a.input = input;
+    a.rms_weight = rms_weight;
+    a.epsilon = epsilon;
+    a.input_width = input_width;
+    a.segments = segments;
+    for (uint32_t i = 0; i < segments; ++i) {
+        if (!weights[i] || !outputs[i]) return invalid(ctx, "matvec weights/output is null");
+        if (reinterpret_cast<uintptr_t>(weights[i]) & 1) return invalid(ctx, "Q4_0 weights must be 2-byte aligned");
+        if (widths[i] == 0) return invalid(ctx, "matvec output width is zero");
+        a.weights[i] = weights[i];
+        a.output[i] = outputs[i];
+        a.width[i] = widths[i];
+    }
+    return launched(ctx, atlas::launch_q4_0_matvec(ctx->stream, a), op);
+}
+
+int atlas_hip_matvec_q4_0_rms_f32(atlas_hip_ctx* ctx, const float* input, const uint8_t* weights, float* output,
+                                  uint32_t input_width, uint32_t output_width, const float* rms_weight,
+                                  float epsilon) {
+    const uint8_t* w[1] = {weights};
+    float* o[1] = {output};
+    const uint32_t n[1] = {output_width};
+    return q4_matvec(ctx, input, rms_weight, epsilon, input_width, 1, w, o, n, "matvec_q4_0_rms");
+}
+
+int atlas_hip_matmul_q4_0_qkv_rms_f32(atlas_hip_ctx* ctx, const float* input, const uint8_t* q_weights,
+                                      const uint8_t* k_weights, const uint8_t* v_weights, float* q_output,
+                                      float* k_output, float* v_output, uint32_t input_width, uint32_t q_width,
+                                      uint32_t kv_width, const float* rms_weight, float epsilon) {
+    const uint8_t* w[3] = {q_weights, k_weights, v_weights};
+    float* o[3] = {q_output, k_output, v_output};
+    const uint32_t n[3] = {q_width, kv_width, kv_width};
+    return q4_matvec(ctx, input, rms_weight, epsilon, input_width, 3, w, o, n, "matmul_q4_0_qkv_rms");
+}
+
+int atlas_hip_matmul_q4_0_gate_up_rms_f32(atlas_hip_ctx* ctx, const float* input, const uint8_t* gate_weights,
+                                          const uint8_t* up_weights, float* gate_output, float* up_output,
+                                          uint32_t input_width, uint32_t output_width, const float* rms_weight,
+                                          float epsilon) {
+    const uint8_t* w[2] = {gate_weights, up_weights};
+    float* o[2] = {gate_output, up_output};
+    const uint32_t n[2] = {output_width, output_width};
+    return q4_matvec(ctx, input, rms_weight, epsilon, input_width, 2, w, o, n, "matmul_q4_0_gate_up_rms");
+}
+
 int atlas_hip_ple_q4_0(atlas_hip_ctx* ctx, const uint8_t* table, const uint32_t* ids, const float* projection,
                        float* output, uint32_t vocab, uint32_t layers, uint32_t width, uint32_t tokens,
                        float embedding_scale, float output_scale) {

@@ -91,4 +91,21 @@ hipError_t launch_ple_quant(hipStream_t stream, int q6k, const uint8_t* table, c
                             uint32_t width, uint32_t tokens, float embedding_scale,
                             float output_scale);
 
+// RMS-folded Q4_0 projections of one token (matvec_kernels.hip).  Up to
+// three projections of the same input share one launch (fused QKV, fused
+// gate/up); rms_weight == nullptr gives the plain matvec.
+struct MatvecArgs {
+    const float* input;
+    const float* rms_weight;
+    float epsilon;
+    uint32_t input_width;  // multiple of 32, <= q4_0_matvec_max_input()
+    uint32_t segments;     // 1..3
+    const uint8_t* weights[3];
+    float* output[3];
+    uint32_t width[3];
+    uint32_t tile_begin[3];  // filled by the launcher
+};
+uint32_t q4_0_matvec_max_input();
+hipError_t launch_q4_0_matvec(hipStream_t stream, MatvecArgs a);
+
 }  // namespace atlas

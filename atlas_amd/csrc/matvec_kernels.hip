@@ -1,0 +1,272 @@
+// matvec_kernels.hip -- RMS-folded Q4_0 decode projections for gfx950.
+//
+// Reference semantics (bisegni/atlas, crates/atlas-metal/src/kernels.metal):
+//   matvec_q4_0_16row_mv_rms           :3786-3864  one projection
+//   matmul_q4_0_qkv_16row_mv_rms       :3368-3467  Q, K and V in one dispatch
+//   matmul_q4_0_gate_up_16row_mv_rms   :3468-3564  gate and up in one dispatch
+//   callers crates/atlas-model/src/gemma4_executor.rs:2082-2119, 2502-2612
+//
+// One decode token: output[o] = inv_rms(x) * sum_k (x_k * w_k) * deq(W[o, k]),
+// with inv_rms(x) = 1 / sqrt(sum_k x_k^2 / n + eps) -- the RMS normalisation
+// of the input folded into the dispatch (its scalar applied once per output,
+// as the reference does).  Without an RMS weight it is the plain Q4_0 matvec.
+// Q4_0 rows are 18-byte blocks of 32 values (f16 scale d, 16 bytes; value
+// j < 16 is the low nibble of byte j, value j + 16 its high nibble, minus 8).
+// The reference pins these kernels with a tolerance contract against a
+// normalise-then-matvec CPU oracle (crates/atlas-metal/tests/
+// matvec_rms_fused_parity.rs: max-abs < 1e-3); the summation order here is
+// this kernel's own, deterministic run to run.
+//
+// Layout on CDNA: the op streams the weight matrix once (it is HBM-bound;
+// MFMA does not apply to one token).  One wavefront owns a tile of 16
+// consecutive output rows -- a contiguous byte range of the weight matrix --
+// and stages it into LDS with 128-bit loads, all issued before the first
+// wait.  Meanwhile the lanes form y = x * w (the normalised input before its
+// scalar) in LDS with the per-block sums of y and the row sum of squares.
+// Lane (g, s), g < 64/LPR, s < LPR, then keeps the y values of blocks
+// s, s + LPR, ... in registers and applies them to rows g, g + 64/LPR, ...
+// of the tile: 16 nibbles per byte pair decoded with masks and
+// v_cvt_f32_ubyte, sum_j q_j * y_j accumulated in f32, and the Q4_0 offset
+// folded as d * (acc - 8 * sum(y)).  The LPR partial sums of a row are
+// reduced with cross-lane shuffles inside the row's lane group.
+#include "device_common.hpp"
+#include "launch.hpp"
+
+namespace atlas {
+namespace {
+
+constexpr uint32_t kQ4Block = 18;  // bytes per 32 values
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Stage `bytes` (even) starting at `src` into LDS: 16-byte loads when the
+// source is 16-byte aligned (the tail in 2-byte units), else 2-byte loads.
+// A pass issues K loads per lane before the first LDS write (K = 4 covers a
+// wavefront's 4 rows of 864 bytes, the Gemma hidden width, in one pass).  Load and store
+// indices are both clamped to the last unit (lanes past the end copy that
+// unit again, writing the value it already holds), so no access is
+// conditional and the compiler cannot sink a load into a guarded store and
+// serialise the pass.
+template <int K, typename U>
+__device__ __forceinline__ void stage_units(uint8_t* dst, const uint8_t* src, uint32_t units, uint32_t lane) {
+    for (uint32_t base = 0; base < units; base += K * kWave) {
+        U v[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) v[k] = reinterpret_cast<const U*>(src)[min(base + lane + k * kWave, units - 1)];
+#pragma unroll
+        for (int k = 0; k < K; ++k) reinterpret_cast<U*>(dst)[min(base + lane + k * kWave, units - 1)] = v[k];
+    }
+}
+
+__device__ __forceinline__ void stage_tile(uint8_t* dst, const uint8_t* src, uint32_t bytes, uint32_t lane) {
+    uint32_t done = 0;
+    if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+        const uint32_t n16 = bytes / 16;
+        if (n16) stage_units<4, uint4>(dst, src, n16, lane);
+        done = n16 * 16;
+    }
+    if (bytes > done) stage_units<8, uint16_t>(dst + done, src + done, (bytes - done) / 2, lane);
+}
+
+// Sum over aligned groups of LPR lanes; every lane of a group gets the total.
+// Inside a 16-lane DPP row the butterfly is quad_perm (xor 1, xor 2),
+// row_half_mirror and row_mirror (VALU ops, no LDS); wider groups add
+// cross-row shuffles.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+template <int LPR>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp_f32<0xb1>(v);                 // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4e>(v);                 // quad_perm [2,3,0,1]
+    if (LPR >= 8) v += dpp_f32<0x141>(v);   // row_half_mirror
+    if (LPR >= 16) v += dpp_f32<0x140>(v);  // row_mirror
+    if (LPR >= 32) v += __shfl_xor(v, 16, kWave);
+    if (LPR >= 64) v += __shfl_xor(v, 32, kWave);
+    return v;
+}
+
+// The Q4_0 block at LDS byte offset `off` (even): its f16 scale d and its
+// 16 quant bytes as four dwords, read with 4-byte LDS loads.  An offset that
+// is 0 mod 4 holds the scale in the low half of the first dword (the five
+// dwords end 2 bytes past the block, still inside the LDS allocation); an
+// offset that is 2 mod 4 holds it in the high half of the dword before the
+// quant bytes, which are then dword aligned.
+__device__ __forceinline__ void load_q4_block(const uint8_t* lds, uint32_t off, float& d, uint32_t (&q)[4]) {
+    if ((off & 3) == 0) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(lds + off);
+        const uint32_t w0 = p[0], w1 = p[1], w2 = p[2], w3 = p[3], w4 = p[4];
+        d = h2f(static_cast<uint16_t>(w0));
+        q[0] = __builtin_amdgcn_alignbit(w1, w0, 16);
+        q[1] = __builtin_amdgcn_alignbit(w2, w1, 16);
+        q[2] = __builtin_amdgcn_alignbit(w3, w2, 16);
+        q[3] = __builtin_amdgcn_alignbit(w4, w3, 16);
+    } else {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(lds + off - 2);
+        d = h2f(static_cast<uint16_t>(p[0] >> 16));
+        q[0] = p[1];
+        q[1] = p[2];
+        q[2] = p[3];
+        q[3] = p[4];
+    }
+}
+
+// sum_j q_j * y_j over one Q4_0 block's 32 values (nibble codes 0..15):
+// byte j of q holds codes j (low nibble) and j + 16 (high nibble).
+__device__ __forceinline__ float q4_block_dot(const uint32_t (&q)[4], const float (&y)[32]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t lo = q[w] & 0x0f0f0f0fu, hi = (q[w] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {  // byte-wise conversions (v_cvt_f32_ubyte0..3)
+            acc = __builtin_fmaf(static_cast<float>((lo >> (8 * k)) & 0xffu), y[4 * w + k], acc);
+            acc = __builtin_fmaf(static_cast<float>((hi >> (8 * k)) & 0xffu), y[4 * w + k + 16], acc);
+        }
+    }
+    return acc;
+}
+
+constexpr uint32_t kWaves = 4;  // wavefronts per workgroup
+// y is stored block by block with a 36-float stride: the 16 or 32 lanes of
+// a row group read 16-byte pieces of consecutive blocks, and a 144-byte
+// stride puts those pieces on distinct LDS banks (a 128-byte stride would
+// put them all on the same four).
+constexpr uint32_t kYStride = 36;
+
+// LPR lanes per output row (one row per lane group), NBT blocks per lane
+// (blocks per row <= LPR * NBT).  A workgroup owns kWaves * 64 / LPR rows.
+template <int LPR, int NBT>
+__global__ __launch_bounds__(256) void q4_0_matvec_kernel(MatvecArgs a) {
+    constexpr uint32_t kGroups = kWave / LPR;           // rows per wavefront
+    constexpr uint32_t kRows = kWaves * kGroups;        // rows per workgroup
+    constexpr int kJ = (LPR * NBT * 32 / 4 + 255) / 256;  // float4 of x per thread
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const uint32_t g = lane / LPR, s = lane % LPR;
+    const uint32_t n = a.input_width, n4 = n / 4, nb = n / 32, row_bytes = nb * kQ4Block;
+
+    // The projection this workgroup's rows belong to (segments are tile ranges).
+    const uint32_t t = blockIdx.x;
+    const uint32_t si = (a.segments > 2 && t >= a.tile_begin[2]) ? 2 : ((a.segments > 1 && t >= a.tile_begin[1]) ? 1 : 0);
+    const uint8_t* weights = si == 0 ? a.weights[0] : (si == 1 ? a.weights[1] : a.weights[2]);
+    float* out = si == 0 ? a.output[0] : (si == 1 ? a.output[1] : a.output[2]);
+    const uint32_t width = si == 0 ? a.width[0] : (si == 1 ? a.width[1] : a.width[2]);
+    const uint32_t begin = si == 0 ? a.tile_begin[0] : (si == 1 ? a.tile_begin[1] : a.tile_begin[2]);
+    const uint32_t row0 = (t - begin) * kRows;
+    const uint32_t nrows = min(kRows, width - row0);
+    // this wavefront's rows: [wrow0, wrow0 + wrows) of the tile
+    const uint32_t wrow0 = min(wave * kGroups, nrows);
+    const uint32_t wrows = min(kGroups, nrows - wrow0);
+
+    uint8_t* tile = smem;                                                         // kRows * row_bytes
+    float* ys = reinterpret_cast<float*>(smem + ((kRows * row_bytes + 15) & ~15u));  // nb * kYStride floats
+    float* block_sums = ys + nb * kYStride;                                       // nb floats
+    float* partial = block_sums + nb;                                             // kWaves floats
+
+    // 1. input and RMS weight: every load of the workgroup issued up front
+    //    (indices clamped, duplicates not stored)
+    const bool rms = a.rms_weight != nullptr;
+    f32x4 xv[kJ], wv[kJ];
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+        const uint32_t c = min(tid + 256u * j, n4 - 1);
+        xv[j] = reinterpret_cast<const f32x4*>(a.input)[c];
+        wv[j] = rms ? reinterpret_cast<const f32x4*>(a.rms_weight)[c] : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+    }
+
+    // 2. this wavefront's weight rows (the dominant stream), staged into LDS
+    if (wrows) stage_tile(tile + wrow0 * row_bytes, weights + static_cast<size_t>(row0 + wrow0) * row_bytes,
+                          wrows * row_bytes, lane);
+
+    // 3. y = x * w (or x), the per-block sums of y (a block is 8 float4, held
+    //    by 8 consecutive threads) and the sum of squares
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+        const uint32_t c = min(tid + 256u * j, n4 - 1);  // duplicates recompute the last float4
+        const f32x4 x = xv[j], w = wv[j];
+        f32x4 y = x;
+        if (rms) y = f32x4{x.x * w.x, x.y * w.y, x.z * w.z, x.w * w.w};
+        const float bsum = group_sum<8>((y.x + y.y) + (y.z + y.w));
+        if (tid + 256u * j < n4) {
+            if (rms) ss = ss + x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+            *reinterpret_cast<f32x4*>(ys + (c / 8) * kYStride + 4 * (c % 8)) = y;
+            if (c % 8 == 0) block_sums[c / 8] = bsum;
+        }
+    }
+    ss = group_sum<kWave>(ss);
+    if (lane == 0) partial[wave] = ss;
+    __syncthreads();
+    float inv = 1.0f;
+    if (rms) inv = inverse_rms((partial[0] + partial[1]) + (partial[2] + partial[3]), static_cast<float>(n), a.epsilon);
+
+    // 4. lane (g, s): row wrow0 + g, blocks s + LPR * i
+    const uint32_t row = wrow0 + g;
+    float acc = 0.0f;
+    if (g < wrows) {
+        const uint32_t row_off = row * row_bytes;
+#pragma unroll
+        for (int i = 0; i < NBT; ++i) {
+            const uint32_t b = s + LPR * i;
+            if (b < nb) {
+                float y[32];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(ys + kYStride * b + 4 * k);
+                    y[4 * k] = v.x;
+                    y[4 * k + 1] = v.y;
+                    y[4 * k + 2] = v.z;
+                    y[4 * k + 3] = v.w;
+                }
+                float d;
+                uint32_t q[4];
+                load_q4_block(tile, row_off + b * kQ4Block, d, q);
+                acc = __builtin_fmaf(d, q4_block_dot(q, y) - 8.0f * block_sums[b], acc);
+            }
+        }
+    }
+    const float total = group_sum<LPR>(acc);
+    if (s == 0 && g < wrows) out[row0 + row] = rms ? total * inv : total;
+}
+
+template <int LPR, int NBT>
+hipError_t launch_lpr(hipStream_t stream, MatvecArgs a) {
+    constexpr uint32_t kRows = kWaves * (kWave / LPR);
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < a.segments; ++i) {
+        a.tile_begin[i] = tiles;
+        tiles += (a.width[i] + kRows - 1) / kRows;
+    }
+    const uint32_t nb = a.input_width / 32;
+    const size_t lds = ((kRows * nb * kQ4Block + 15) & ~15u) + (nb * kYStride + nb + kWaves) * sizeof(float);
+    hipLaunchKernelGGL((q4_0_matvec_kernel<LPR, NBT>), dim3(tiles), dim3(kWaves * kWave), lds, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+uint32_t q4_0_matvec_max_input() { return 32 * 4 * 32; }
+
+hipError_t launch_q4_0_matvec(hipStream_t stream, MatvecArgs a) {
+    const uint32_t nb = a.input_width / 32;
+    uint32_t rows = 0;
+    for (uint32_t i = 0; i < a.segments; ++i) rows += a.width[i];
+    // Lanes per row: 16 (16 rows per workgroup) when that leaves at least
+    // two workgroups per CU and each lane at <= 4 blocks; otherwise 32
+    // (8 rows per workgroup, twice the workgroups for small projections).
+    if (rows >= 16 * 512 && nb <= 64) {
+        if (nb <= 16) return launch_lpr<16, 1>(stream, a);
+        if (nb <= 32) return launch_lpr<16, 2>(stream, a);
+        if (nb <= 48) return launch_lpr<16, 3>(stream, a);
+        return launch_lpr<16, 4>(stream, a);
+    }
+    if (nb <= 32) return launch_lpr<32, 1>(stream, a);
+    if (nb <= 64) return launch_lpr<32, 2>(stream, a);
+    if (nb <= 96) return launch_lpr<32, 3>(stream, a);
+    return launch_lpr<32, 4>(stream, a);
+}
+
+}  // namespace atlas

@@ -267,6 +267,23 @@ class HipRuntime:
         self._check(self.lib.atlas_hip_ple_q6_k(self.ctx, _ptr(table), _ptr(ids), _ptr(proj), _ptr(out), vocab, layers,
                                                 width, tokens, emb_scale, out_scale))
 
+    # RMS-folded Q4_0 decode projections (matvec_q4_0_16row_mv_rms and the fused
+    # QKV / gate-up dispatches, kernels.metal:3368-3564, 3786-3864); rms_weight
+    # None gives the plain Q4_0 matvec.
+    def matvec_q4_0_rms(self, x, weights, out, input_width, output_width, rms_weight, eps):
+        self._check(self.lib.atlas_hip_matvec_q4_0_rms_f32(self.ctx, _ptr(x), _ptr(weights), _ptr(out), input_width,
+                                                           output_width, _ptr(rms_weight), eps))
+
+    def matmul_q4_0_qkv_rms(self, x, qw, kw, vw, q_out, k_out, v_out, input_width, q_width, kv_width, rms_weight, eps):
+        self._check(self.lib.atlas_hip_matmul_q4_0_qkv_rms_f32(self.ctx, _ptr(x), _ptr(qw), _ptr(kw), _ptr(vw),
+                                                               _ptr(q_out), _ptr(k_out), _ptr(v_out), input_width,
+                                                               q_width, kv_width, _ptr(rms_weight), eps))
+
+    def matmul_q4_0_gate_up_rms(self, x, gw, uw, g_out, u_out, input_width, output_width, rms_weight, eps):
+        self._check(self.lib.atlas_hip_matmul_q4_0_gate_up_rms_f32(self.ctx, _ptr(x), _ptr(gw), _ptr(uw), _ptr(g_out),
+                                                                   _ptr(u_out), input_width, output_width,
+                                                                   _ptr(rms_weight), eps))
+
 
 def rope_tables_gemma4(positions, rope_pairs, rotary, theta, frequency_factors=None):
     """Host cos/sin tables [tokens, rope_pairs] (gemma4_executor.rs:622-633, 3494-3519)."""

@@ -128,7 +128,8 @@ class Ops:
 class ConfigOps(Ops):
     """Per-op timing at the other op configurations (separate lines, not the headline):
     c1 = BASELINE configs[0] (SmolLM2-135M-shaped FP32 ops, T=128),
-    c2 = BASELINE configs[1] (SmolLM2-1.7B-shaped FP16 storage, T=2048)."""
+    c2 = BASELINE configs[1] (SmolLM2-1.7B-shaped FP16 storage, T=2048),
+    gemv = the RMS-folded Q4_0 decode projections of one Gemma-4-E2B-like token."""
 
     def __init__(self, wl, rope_tables, cfg):
         r = wl.rng(2025)
@@ -155,6 +156,26 @@ class ConfigOps(Ops):
                                                                      D // 2))),
                 "swiglu_f16": (["gate", "up"], {"o": T * F // 2}, 3 * T * F * 2,
                                lambda rt, s: rt.swiglu_f16(s["gate"], s["up"], s["o"], T * F)),
+            }
+        elif cfg == "gemv":
+            # the RMS-folded Q4_0 decode projections of one
+            # Gemma-4-E2B-like token (hidden 1536; Q 8x256, K/V 1x256; FFN 6144)
+            L = wl.GemmaLayerShape()
+            H, QN, KVN, F = L.hidden, L.q_heads * L.head_dim, L.head_dim, L.ffn
+            rb = wl.q_row_bytes(H, False)
+            self.tokens = 1
+            self.host = {"x": wl.normal(r, H), "w": wl.normal(r, H, 1.0, 0.1), "qw": wl.q4_0_table(r, QN, H),
+                         "kw": wl.q4_0_table(r, KVN, H), "vw": wl.q4_0_table(r, KVN, H),
+                         "gw": wl.q4_0_table(r, F, H), "uw": wl.q4_0_table(r, F, H)}
+            eps = L.eps
+            self.table = {
+                "qkv_rms": (["x", "w", "qw", "kw", "vw"], {"qo": QN, "ko": KVN, "vo": KVN},
+                            (QN + 2 * KVN) * rb + 2 * H * 4 + (QN + 2 * KVN) * 4,
+                            lambda rt, s: rt.matmul_q4_0_qkv_rms(s["x"], s["qw"], s["kw"], s["vw"], s["qo"], s["ko"],
+                                                                 s["vo"], H, QN, KVN, s["w"], eps)),
+                "gate_up_rms": (["x", "w", "gw", "uw"], {"go": F, "uo": F}, 2 * F * rb + 2 * H * 4 + 2 * F * 4,
+                                lambda rt, s: rt.matmul_q4_0_gate_up_rms(s["x"], s["gw"], s["uw"], s["go"], s["uo"],
+                                                                         H, F, s["w"], eps)),
             }
         else:
             S = wl.SmolShape()
@@ -303,8 +324,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma-separated op subset: per-op timing only (profiling)")
     ap.add_argument("--copy-mib", type=int, default=0, help="also time a device-to-device copy of this size")
-    ap.add_argument("--config", choices=["c3c4", "c1", "c2"], default="c3c4",
-                    help="c1 / c2: per-op lines for BASELINE configs[0] / configs[1] instead of the headline")
+    ap.add_argument("--config", choices=["c3c4", "c1", "c2", "gemv"], default="c3c4",
+                    help="c1 / c2: per-op lines for BASELINE configs[0] / configs[1]; gemv: the RMS-folded "
+                         "Q4_0 decode projections of one token -- instead of the headline")
     ap.add_argument("--decode", action="store_true",
                     help="BASELINE configs[4] batched decode (per-layer latency, eager and HIP graph) instead")
     args = ap.parse_args()
@@ -328,7 +350,10 @@ def main():
         cops = ConfigOps(wl, rope_tables_llama, args.config)
         per_op = {}
         for name, (_, _, nbytes, launch) in cops.table.items():
-            nsets = min(64, max(4, math.ceil(ROTATION_BYTES / cops.set_bytes(name))))
+            # the weight-streaming projections need >= 1 GiB of distinct weights
+            # to keep the 256 MB MALL out of the measurement
+            cap = 1024 if args.config == "gemv" else 64
+            nsets = min(cap, max(4, math.ceil(ROTATION_BYTES / cops.set_bytes(name))))
             log(f"timing {args.config} {name} ({nsets} rotating sets)")
             sets = cops.build_sets(rt, [name], nsets)
             ms = time_launches(rt, launch, sets, args.op_iters)

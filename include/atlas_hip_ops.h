@@ -269,6 +269,38 @@ int atlas_hip_ple_q6_k(atlas_hip_ctx *ctx, const uint8_t *table, const uint32_t 
                        const float *projection, float *output, uint32_t vocab, uint32_t layers,
                        uint32_t width, uint32_t tokens, float embedding_scale, float output_scale);
 
+/* ---- RMS-folded Q4_0 decode projections (one token) --------------------- */
+
+/* output[o] = inv_rms(input) * sum_k (input[k] * rms_weight[k]) * deq(W[o, k])
+ * with inv_rms = 1 / sqrt(sum_k input[k]^2 / input_width + epsilon): the
+ * RMS-normalised input of a decode step folded into its projection.  With
+ * rms_weight == NULL it is the plain Q4_0 matvec (output = W . input).
+ * W is [output_width, input_width] in Q4_0 blocks (18 bytes per 32 values,
+ * rows contiguous); input_width is a multiple of 32 and at most 4096;
+ * input and rms_weight are 16-byte aligned f32 vectors, W is 2-byte aligned
+ * (16-byte aligned takes the wide staging path).  Floating-point parity is
+ * the reference's own contract (normalise-then-matvec CPU oracle, max-abs
+ * < 1e-3, crates/atlas-metal/tests/matvec_rms_fused_parity.rs).
+ * matvec_q4_0_16row_mv_rms (kernels.metal:3786-3864); caller
+ * Gemma4Executor::matvec_rms_labeled (gemma4_executor.rs:2082-2119). */
+int atlas_hip_matvec_q4_0_rms_f32(atlas_hip_ctx *ctx, const float *input, const uint8_t *weights,
+                                  float *output, uint32_t input_width, uint32_t output_width,
+                                  const float *rms_weight, float epsilon);
+/* matmul_q4_0_qkv_16row_mv_rms (kernels.metal:3368-3467; caller
+ * Gemma4Executor::matmul_q4_0_qkv, gemma4_executor.rs:2502-2558): the Q, K and
+ * V projections of one input in one launch; K and V share kv_width. */
+int atlas_hip_matmul_q4_0_qkv_rms_f32(atlas_hip_ctx *ctx, const float *input, const uint8_t *q_weights,
+                                      const uint8_t *k_weights, const uint8_t *v_weights, float *q_output,
+                                      float *k_output, float *v_output, uint32_t input_width,
+                                      uint32_t q_width, uint32_t kv_width, const float *rms_weight,
+                                      float epsilon);
+/* matmul_q4_0_gate_up_16row_mv_rms (kernels.metal:3468-3564; caller
+ * Gemma4Executor::matmul_q4_0_gate_up, gemma4_executor.rs:2560-2612). */
+int atlas_hip_matmul_q4_0_gate_up_rms_f32(atlas_hip_ctx *ctx, const float *input,
+                                          const uint8_t *gate_weights, const uint8_t *up_weights,
+                                          float *gate_output, float *up_output, uint32_t input_width,
+                                          uint32_t output_width, const float *rms_weight, float epsilon);
+
 /* ---- host-slice operator API (atlas_ops::NeuralOps) --------------------- */
 
 /* NeuralOps::embedding -> MetalRuntime::embedding_lookup (lib.rs:1393-1433). */

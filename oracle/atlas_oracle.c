@@ -633,3 +633,73 @@ void oracle_multiply_f32(const float *lhs, const float *rhs, float *output, size
 void oracle_scale_f32(const float *input, float scalar, float *output, size_t n) {
     for (size_t i = 0; i < n; ++i) output[i] = input[i] * scalar;
 }
+
+/* ======================================================================== */
+/* RMS-folded Q4_0 decode projections                                       */
+/* ======================================================================== */
+
+/* The reference's own CPU oracle for the _rms matvec kernels
+ * (crates/atlas-metal/tests/matvec_rms_fused_parity.rs:51-80), in f32:
+ * cpu_rms_normalize -- mean_sq = (sequential sum of x*x) / n,
+ * inv = 1 / sqrt(mean_sq + eps), normalized = (x * w) * inv -- then
+ * cpu_q4_matvec -- acc += normalized[k] * dequantize_block(...)[lane],
+ * blocks and lanes in order.  rms_weight == NULL: the plain matvec of x. */
+void oracle_matvec_q4_0_rms_ref(const float *input, const uint8_t *weights, const float *rms_weight,
+                                size_t input_width, size_t output_width, float epsilon, float *output) {
+    const size_t blocks = input_width / 32;
+    float normalized[8192];
+    if (input_width > 8192) return;
+    if (rms_weight) {
+        float sum = 0.0f;
+        for (size_t k = 0; k < input_width; ++k) sum = sum + input[k] * input[k];
+        const float mean_sq = sum / (float)input_width;
+        const float inv = 1.0f / sqrtf(mean_sq + epsilon);
+        for (size_t k = 0; k < input_width; ++k) normalized[k] = input[k] * rms_weight[k] * inv;
+    } else {
+        for (size_t k = 0; k < input_width; ++k) normalized[k] = input[k];
+    }
+    float block[32];
+    for (size_t row = 0; row < output_width; ++row) {
+        float acc = 0.0f;
+        for (size_t b = 0; b < blocks; ++b) {
+            oracle_dequant_q4_0_block(weights + (row * blocks + b) * 18, block);
+            for (size_t lane = 0; lane < 32; ++lane) acc = acc + normalized[b * 32 + lane] * block[lane];
+        }
+        output[row] = acc;
+    }
+}
+
+/* The same projection in float64 from the same f32 inputs: the exact value
+ * of inv_rms(x) * sum_k (x_k * w_k) * deq_k up to float64 rounding, and
+ * magnitude[o] = inv * sum_k 16 * |x_k * w_k * d_block(k)|, a bound on every
+ * partial sum an f32 evaluation forms (codes q in [0, 15], offset 8), i.e.
+ * the scale of its rounding error in any summation order. */
+void oracle_matvec_q4_0_rms_f64(const float *input, const uint8_t *weights, const float *rms_weight,
+                                size_t input_width, size_t output_width, float epsilon, double *output,
+                                double *magnitude) {
+    const size_t blocks = input_width / 32;
+    double inv = 1.0;
+    if (rms_weight) {
+        double sum = 0.0;
+        for (size_t k = 0; k < input_width; ++k) sum += (double)input[k] * (double)input[k];
+        inv = 1.0 / sqrt(sum / (double)input_width + (double)epsilon);
+    }
+    float block[32];
+    for (size_t row = 0; row < output_width; ++row) {
+        double acc = 0.0, mag = 0.0;
+        for (size_t b = 0; b < blocks; ++b) {
+            const uint8_t *blk = weights + (row * blocks + b) * 18;
+            oracle_dequant_q4_0_block(blk, block);
+            const double d = fabs((double)oracle_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8))));
+            for (size_t lane = 0; lane < 32; ++lane) {
+                const size_t k = b * 32 + lane;
+                const double y = (double)input[k] * (rms_weight ? (double)rms_weight[k] : 1.0);
+                acc += y * (double)block[lane];
+                mag += 16.0 * fabs(y) * d;
+            }
+        }
+        output[row] = acc * inv;
+        magnitude[row] = mag * inv;
+    }
+}
+

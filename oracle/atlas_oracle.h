@@ -143,6 +143,14 @@ void oracle_multiply_f32(const float *lhs, const float *rhs, float *output,
                          size_t n);
 void oracle_scale_f32(const float *input, float scalar, float *output, size_t n);
 
+/* RMS-folded Q4_0 decode projections (matvec_rms_fused_parity.rs:51-80
+ * oracle in f32, and a float64 restatement with the error magnitude). */
+void oracle_matvec_q4_0_rms_ref(const float *input, const uint8_t *weights, const float *rms_weight,
+                                size_t input_width, size_t output_width, float epsilon, float *output);
+void oracle_matvec_q4_0_rms_f64(const float *input, const uint8_t *weights, const float *rms_weight,
+                                size_t input_width, size_t output_width, float epsilon, double *output,
+                                double *magnitude);
+
 #ifdef __cplusplus
 }
 #endif

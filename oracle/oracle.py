@@ -58,6 +58,8 @@ _SIGS = {
     "oracle_ple_q4_0": ([P, P, P, P, SZ, SZ, SZ, SZ, F, F], None),
     "oracle_ple_q6_k": ([P, P, P, P, SZ, SZ, SZ, SZ, F, F], None),
     "oracle_combine_ple": ([P, P, P, SZ], None),
+    "oracle_matvec_q4_0_rms_ref": ([P, P, P, SZ, SZ, F, P], None),
+    "oracle_matvec_q4_0_rms_f64": ([P, P, P, SZ, SZ, F, P, P], None),
     "oracle_add_f32": ([P, P, P, SZ], None),
     "oracle_multiply_f32": ([P, P, P, SZ], None),
     "oracle_scale_f32": ([P, F, P, SZ], None),
@@ -330,3 +332,25 @@ def scale(a, s):
     out = np.empty(a.size, f32)
     lib().oracle_scale_f32(_p(a), s, _p(out), a.size)
     return out
+
+
+def matvec_q4_0_rms_ref(x, weights, rms_weight, input_width, output_width, eps):
+    """The reference test's f32 oracle: normalise, then Q4_0 matvec in order
+    (crates/atlas-metal/tests/matvec_rms_fused_parity.rs:51-80)."""
+    xx, ww = _c(x, f32), _c(weights, u8)
+    rw = None if rms_weight is None else _c(rms_weight, f32)
+    out = np.zeros(output_width, f32)
+    lib().oracle_matvec_q4_0_rms_ref(_p(xx), _p(ww), None if rw is None else _p(rw), input_width, output_width, eps,
+                                     _p(out))
+    return out
+
+
+def matvec_q4_0_rms_f64(x, weights, rms_weight, input_width, output_width, eps):
+    """float64 value of the projection and its error magnitude inv * sum |terms|."""
+    xx, ww = _c(x, f32), _c(weights, u8)
+    rw = None if rms_weight is None else _c(rms_weight, f32)
+    out, mag = np.zeros(output_width, np.float64), np.zeros(output_width, np.float64)
+    lib().oracle_matvec_q4_0_rms_f64(_p(xx), _p(ww), None if rw is None else _p(rw), input_width, output_width, eps,
+                                     _p(out), _p(mag))
+    return out, mag
+

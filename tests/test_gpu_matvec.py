@@ -1,0 +1,172 @@
+"""GPU tests of the RMS-folded Q4_0 decode projections (matvec, fused QKV,
+fused gate/up) through the C ABI.
+
+Parity is floating-point, so two tolerances are asserted:
+  * the reference's own contract (crates/atlas-metal/tests/
+    matvec_rms_fused_parity.rs): max |gpu - oracle| < 1e-3 against the f32
+    normalise-then-matvec oracle, on the reference test's own seeded inputs;
+  * a normwise bound against the float64 oracle: |gpu - exact| <= 1e-5 *
+    magnitude, where magnitude = inv_rms * sum_k 16 |x_k w_k d_k| bounds every
+    partial sum an f32 evaluation forms (TOL below).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import matvec_cases as mc
+from atlas_amd import OperatorError
+
+pytestmark = pytest.mark.gpu
+f32 = np.float32
+EPS = 1e-6
+TOL = 1e-5       # normwise, against the float64 oracle
+REF_TOL = 1e-3   # the reference's max-abs contract against its f32 oracle
+
+
+def say(msg):
+    print(f"[gpu-matvec] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def check(name, got, ora, x, W, w, n, rows, ref_contract=False):
+    exact, mag = ora.matvec_q4_0_rms_f64(x, W, w, n, rows, EPS)
+    err = np.abs(got.astype(np.float64) - exact)
+    worst = float(np.max(err / np.maximum(mag, 1e-300)))
+    assert np.all(err <= TOL * mag), f"{name}: normwise error {worst:.3e} > {TOL}"
+    if ref_contract:
+        ref = ora.matvec_q4_0_rms_ref(x, W, w, n, rows, EPS)
+        max_abs = float(np.max(np.abs(got - ref)))
+        assert max_abs < REF_TOL, f"{name}: max_abs {max_abs:.3e} against the reference oracle"
+    return worst
+
+
+def run_qkv(rt, x, qw, kw, vw, w, n, qn, kvn):
+    dx, dw = rt.upload(x), (rt.upload(w) if w is not None else None)
+    dq, dk, dv = rt.upload(qw), rt.upload(kw), rt.upload(vw)
+    oq, ok, ov = rt.empty(qn), rt.empty(kvn), rt.empty(kvn)
+    rt.matmul_q4_0_qkv_rms(dx, dq, dk, dv, oq, ok, ov, n, qn, kvn, dw, EPS)
+    rt.sync()
+    return oq.download(qn), ok.download(kvn), ov.download(kvn)
+
+
+def run_gate_up(rt, x, gw, uw, w, n, m):
+    dx, dw = rt.upload(x), (rt.upload(w) if w is not None else None)
+    dg, du = rt.upload(gw), rt.upload(uw)
+    og, ou = rt.empty(m), rt.empty(m)
+    rt.matmul_q4_0_gate_up_rms(dx, dg, du, og, ou, n, m, dw, EPS)
+    rt.sync()
+    return og.download(m), ou.download(m)
+
+
+def run_matvec(rt, x, W, w, n, m, weight_offset=0):
+    dx, dw = rt.upload(x), (rt.upload(w) if w is not None else None)
+    raw = np.zeros(W.size + weight_offset, np.uint8)
+    raw[weight_offset:] = W
+    dW = rt.upload(raw)
+    out = rt.empty(m)
+    rt.matvec_q4_0_rms(dx, dW.ptr + weight_offset, out, n, m, dw, EPS)
+    rt.sync()
+    return out.download(m)
+
+
+def test_qkv_reference_test_inputs(rt, ora):
+    """qkv_32row_mv_rms_matches_cpu_oracle (matvec_rms_fused_parity.rs:106-198):
+    same LCG stream, widths and weight builder."""
+    lcg = mc.Lcg(0x9E3779B9)
+    for n in (128, 256, 2048):
+        x = mc.reference_fill_f32(n, lcg)
+        w = mc.reference_fill_rms_weight(n, lcg)
+        for qn, kvn in ((96, 96), (128, 128), (512, 128), (513, 129)):
+            say(f"qkv reference inputs n={n} q={qn} kv={kvn}")
+            qw, kw, vw = (mc.reference_q4_weights(r, n // 32) for r in (qn, kvn, kvn))
+            q, k, v = run_qkv(rt, x, qw, kw, vw, w, n, qn, kvn)
+            check("q", q, ora, x, qw, w, n, qn, True)
+            check("k", k, ora, x, kw, w, n, kvn, True)
+            check("v", v, ora, x, vw, w, n, kvn, True)
+
+
+def test_gate_up_reference_test_inputs(rt, ora):
+    """gate_up_32row_mv_rms_matches_cpu_oracle (matvec_rms_fused_parity.rs:200-267)."""
+    lcg = mc.Lcg(0x9E3779B9)
+    for n in (128, 256, 2048):
+        x = mc.reference_fill_f32(n, lcg)
+        w = mc.reference_fill_rms_weight(n, lcg)
+        for m in (96, 512, 513, 129):
+            say(f"gate_up reference inputs n={n} out={m}")
+            gw, uw = mc.reference_q4_weights(m, n // 32), mc.reference_q4_weights(m, n // 32)
+            g, u = run_gate_up(rt, x, gw, uw, w, n, m)
+            check("gate", g, ora, x, gw, w, n, m, True)
+            check("up", u, ora, x, uw, w, n, m, True)
+
+
+@pytest.mark.parametrize("n,qn,kvn", [(1536, 2048, 256), (1536, 4096, 512), (2048, 2048, 512), (576, 576, 192),
+                                      (32, 17, 1), (4096, 64, 16), (1024, 1000, 33)])
+def test_qkv_shapes(rt, ora, n, qn, kvn):
+    """Gemma-4-E2B (1536 -> 8x256 / 1x256; full layers 1536 -> 8x512 / 1x512),
+    SmolLM2 (2048, 576) and edge widths (one block, 4096, ragged tiles)."""
+    r = np.random.default_rng(100 + n + qn)
+    x = r.standard_normal(n).astype(f32)
+    w = (1.0 + 0.1 * r.standard_normal(n)).astype(f32)
+    qw, kw, vw = mc.random_q4_0(r, qn, n), mc.random_q4_0(r, kvn, n), mc.random_q4_0(r, kvn, n)
+    say(f"qkv shapes n={n} q={qn} kv={kvn}")
+    q, k, v = run_qkv(rt, x, qw, kw, vw, w, n, qn, kvn)
+    worst = max(check("q", q, ora, x, qw, w, n, qn), check("k", k, ora, x, kw, w, n, kvn),
+                check("v", v, ora, x, vw, w, n, kvn))
+    say(f"  worst normwise error {worst:.2e}")
+
+
+@pytest.mark.parametrize("n,m", [(1536, 6144), (2048, 8192), (576, 1536), (4096, 100), (64, 3)])
+def test_gate_up_shapes(rt, ora, n, m):
+    r = np.random.default_rng(200 + n + m)
+    x = r.standard_normal(n).astype(f32)
+    w = (1.0 + 0.1 * r.standard_normal(n)).astype(f32)
+    gw, uw = mc.random_q4_0(r, m, n), mc.random_q4_0(r, m, n)
+    say(f"gate_up shapes n={n} out={m}")
+    g, u = run_gate_up(rt, x, gw, uw, w, n, m)
+    check("gate", g, ora, x, gw, w, n, m)
+    check("up", u, ora, x, uw, w, n, m)
+
+
+@pytest.mark.parametrize("rms", [True, False])
+@pytest.mark.parametrize("offset", [0, 2, 18])
+def test_matvec_single_and_unaligned_weights(rt, ora, rms, offset):
+    """matvec_q4_0_16row_mv_rms and the plain matvec (no RMS weight); weights at
+    2-byte (not 16-byte) aligned addresses take the narrow staging path."""
+    r = np.random.default_rng(300 + offset)
+    n, m = 1536, 777
+    x = (3.0 * r.standard_normal(n)).astype(f32)
+    w = (1.0 + 0.1 * r.standard_normal(n)).astype(f32) if rms else None
+    W = mc.random_q4_0(r, m, n)
+    say(f"matvec rms={rms} weight offset={offset}")
+    got = run_matvec(rt, x, W, w, n, m, offset)
+    check("matvec", got, ora, x, W, w, n, m)
+
+
+def test_matvec_deterministic(rt, ora):
+    r = np.random.default_rng(9)
+    n, m = 1536, 2048
+    x, w, W = r.standard_normal(n).astype(f32), r.standard_normal(n).astype(f32), mc.random_q4_0(r, m, n)
+    say("matvec run-to-run determinism")
+    a = run_matvec(rt, x, W, w, n, m)
+    b = run_matvec(rt, x, W, w, n, m)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_matvec_invalid_input(rt):
+    """InvalidInput before any device work (widths, alignment, epsilon, null buffers)."""
+    say("matvec invalid input")
+    x, out = rt.empty(4096 + 64), rt.empty(64)
+    W = rt.empty(64 * 8)
+    w = rt.empty(4096)
+    for bad in (lambda: rt.matvec_q4_0_rms(x, W, out, 100, 4, w, EPS),           # not a multiple of 32
+                lambda: rt.matvec_q4_0_rms(x, W, out, 4096 + 32, 4, w, EPS),     # wider than 4096
+                lambda: rt.matvec_q4_0_rms(x, W, out, 0, 4, w, EPS),
+                lambda: rt.matvec_q4_0_rms(x, W, out, 64, 0, w, EPS),
+                lambda: rt.matvec_q4_0_rms(x.ptr + 4, W, out, 64, 4, w, EPS),    # misaligned input
+                lambda: rt.matvec_q4_0_rms(x, W.ptr + 1, out, 64, 4, w, EPS),    # odd weight address
+                lambda: rt.matvec_q4_0_rms(x, W, out, 64, 4, w, 0.0),            # epsilon
+                lambda: rt.matvec_q4_0_rms(x, None, out, 64, 4, w, EPS)):
+        with pytest.raises(OperatorError) as e:
+            bad()
+        assert e.value.kind == "InvalidInput"

@@ -400,3 +400,53 @@ def test_pins_catch_planted_mistakes(ora):
     wrong_scale_index = b.copy()
     wrong_scale_index[192] = 2  # scale of group 0 only: a wrong index must change values
     assert not np.array_equal(ora.dequant_q6_k_block(b), ora.dequant_q6_k_block(wrong_scale_index))
+
+
+# ------------------------------------------------ RMS-folded Q4_0 projections
+
+def test_matvec_q4_0_oracles_pinned(ora):
+    """The f64 oracle equals an independent numpy decode + float64 matvec; the
+    f32 reference-test oracle (normalise, then sequential matvec) stays within
+    the sequential-accumulation bound of it; a one-hot input has a closed form."""
+    import matvec_cases as mc
+    r = np.random.default_rng(31)
+    n, rows, eps = 256, 40, 1e-6
+    x = r.standard_normal(n).astype(f32)
+    w = (1.0 + 0.1 * r.standard_normal(n)).astype(f32)
+    W = mc.random_q4_0(r, rows, n)
+    deq = mc.q4_0_dequant_numpy(W, rows, n)
+    inv = 1.0 / np.sqrt(np.sum(x.astype(np.float64) ** 2) / n + eps)
+    exp = (deq @ (x.astype(np.float64) * w.astype(np.float64))) * inv
+    got64, mag = ora.matvec_q4_0_rms_f64(x, W, w, n, rows, eps)
+    np.testing.assert_allclose(got64, exp, rtol=1e-12, atol=1e-12 * float(mag.max()))
+    ref32 = ora.matvec_q4_0_rms_ref(x, W, w, n, rows, eps)
+    # sequential f32: |err| <= (n + 4) * 2^-24 * sum|terms| (sum|terms| <= mag / 2)
+    assert np.all(np.abs(ref32 - got64) <= (n + 8) * 2.0 ** -24 * mag)
+    # plain matvec (no RMS weight) and a one-hot input: output = deq column exactly
+    k = 77
+    e = np.zeros(n, f32)
+    e[k] = 1.0
+    col, _ = ora.matvec_q4_0_rms_f64(e, W, None, n, rows, eps)
+    assert np.array_equal(col, deq[:, k])
+    assert np.array_equal(ora.matvec_q4_0_rms_ref(e, W, None, n, rows, eps), deq[:, k].astype(f32))
+    # one-hot with RMS: x = c e_k -> inv = 1/sqrt(c^2/n + eps), y_k = c w_k
+    c = f32(3.0)
+    got, _ = ora.matvec_q4_0_rms_f64(c * e, W, w, n, rows, eps)
+    np.testing.assert_allclose(got, deq[:, k] * float(c) * float(w[k]) / np.sqrt(9.0 / n + eps), rtol=1e-12)
+
+
+def test_reference_matvec_generators():
+    """The restated reference-test generators reproduce the LCG and the weight
+    pattern of matvec_rms_fused_parity.rs:16-49."""
+    import matvec_cases as mc
+    lcg = mc.Lcg(0x9E3779B9)
+    assert lcg.next_u32() == (0x9E3779B9 * 1664525 + 1013904223) & 0xFFFFFFFF
+    v = mc.reference_fill_f32(1000, mc.Lcg(1))
+    assert v.dtype == np.float32 and v.min() >= -1.0 and v.max() < 1.0
+    W = mc.reference_q4_weights(3, 2).reshape(6, 18)
+    for i in range(6):
+        bits = int(round((0.005 + (i % 101) * 0.0003) * 32768.0))
+        assert W[i, 0] | (W[i, 1] << 8) == bits
+        for j in range(16):
+            nib = (i * 7 + j * 13) % 16
+            assert W[i, 2 + j] == nib | (nib << 4)
