@@ -690,6 +690,44 @@ int atlas_hip_matmul_q4_0_gate_up_rms_f32(atlas_hip_ctx* ctx, const float* input
     return q4_matvec(ctx, input, rms_weight, epsilon, input_width, 2, w, o, n, "matmul_q4_0_gate_up_rms");
 }
 
+static int kv_append(atlas_hip_ctx* ctx, int format, const float* key, const float* value, void* cache,
+                     uint32_t kv_width, uint32_t capacity, const uint32_t* positions, uint32_t tokens, int vnorm,
+                     float epsilon, const char* op) {
+    int rc = enter(ctx);
+    if (rc) return rc;
+    if (!key || !value || !cache || !positions) return invalid(ctx, "KV append buffer is null");
+    if (kv_width == 0 || kv_width > 4096 || capacity == 0 || tokens == 0)
+        return invalid(ctx, "KV append dimensions are invalid (kv_width 1..4096, capacity and tokens > 0)");
+    if (format != atlas::kKvF32 && kv_width % 32 != 0) return invalid(ctx, "quantized KV rows need kv_width % 32 == 0");
+    if (vnorm && kv_width % 4 != 0) return invalid(ctx, "the V norm needs kv_width % 4 == 0");
+    if (vnorm && !finite_positive(epsilon)) return invalid(ctx, "epsilon must be finite and positive");
+    if ((reinterpret_cast<uintptr_t>(key) | reinterpret_cast<uintptr_t>(value)) & 3)
+        return invalid(ctx, "key/value must be 4-byte aligned");
+    if (format == atlas::kKvF32 && (reinterpret_cast<uintptr_t>(cache) & 3)) return invalid(ctx, "f32 cache must be 4-byte aligned");
+    atlas::KvAppendArgs a{key, value, static_cast<uint8_t*>(cache), positions, kv_width, capacity, tokens, epsilon};
+    return launched(ctx, atlas::launch_kv_append(ctx->stream, format, vnorm != 0, a), op);
+}
+
+int atlas_hip_kv_append_f32(atlas_hip_ctx* ctx, const float* key, const float* value, float* cache, uint32_t kv_width,
+                            uint32_t capacity, const uint32_t* positions, uint32_t tokens, int vnorm, float epsilon) {
+    return kv_append(ctx, atlas::kKvF32, key, value, cache, kv_width, capacity, positions, tokens, vnorm, epsilon,
+                     "kv_append_f32");
+}
+
+int atlas_hip_kv_append_q8_0(atlas_hip_ctx* ctx, const float* key, const float* value, uint8_t* cache,
+                             uint32_t kv_width, uint32_t capacity, const uint32_t* positions, uint32_t tokens,
+                             int vnorm, float epsilon) {
+    return kv_append(ctx, atlas::kKvQ8_0, key, value, cache, kv_width, capacity, positions, tokens, vnorm, epsilon,
+                     "kv_append_q8_0");
+}
+
+int atlas_hip_kv_append_q4_0(atlas_hip_ctx* ctx, const float* key, const float* value, uint8_t* cache,
+                             uint32_t kv_width, uint32_t capacity, const uint32_t* positions, uint32_t tokens,
+                             int vnorm, float epsilon) {
+    return kv_append(ctx, atlas::kKvQ4_0, key, value, cache, kv_width, capacity, positions, tokens, vnorm, epsilon,
+                     "kv_append_q4_0");
+}
+
 int atlas_hip_ple_q4_0(atlas_hip_ctx* ctx, const uint8_t* table, const uint32_t* ids, const float* projection,
                        float* output, uint32_t vocab, uint32_t layers, uint32_t width, uint32_t tokens,
                        float embedding_scale, float output_scale) {

@@ -1,0 +1,207 @@
+// kv_kernels.hip -- KV-cache append with the fused V RMSNorm and the
+// Q8_0 / Q4_0 encoders, for gfx950.
+//
+// Reference semantics (bisegni/atlas, crates/atlas-metal/src/kernels.metal):
+//   kv_append_decode_{f32,q8_0,q4_0}          :1197-1267  one token at `position`
+//   kv_append_decode_{f32,q8_0,q4_0}_batch    :1269-1344  tokens with a positions table
+//   kv_append_decode_{f32,q8_0,q4_0}_vnorm    :1346-1436  V RMS-normalised in the same dispatch
+//   rms_norm_groups_in_place_unweighted_f32   :919-929    the unfused V norm
+//   callers crates/atlas-model/src/gemma4_executor.rs:3826-3850 (prefill),
+//           :4326-4368 (decode)
+//
+// Cache layout (the reference's): [K | V][position][row], a row being
+// kv_width f32 values or kv_width/32 blocks of 34 (Q8_0) / 18 (Q4_0) bytes.
+// Tokens whose position is >= capacity are skipped.  With vnorm the V row is
+// scaled by inv = 1 / sqrt(sum_i v_i^2 / kv_width + eps) (sum in index
+// order, as the unfused in-place norm computes it) before it is stored or
+// encoded; the V input buffer itself is left untouched.
+//
+// Encoders (per 32-value block, restating the Metal kernels):
+//   Q8_0: m = max|v|; scale = m == 0 ? 0 : m / 127; code = round-half-away(
+//         clamp(v / scale, -127, 127)); stored: f16(scale) RNE, 32 int8.
+//   Q4_0: the first value with the largest |v| (strictly greater wins) gives
+//         the signed maximum s; scale = s / -8; code = clamp(trunc(v / scale
+//         + 8.5), 0, 15); stored: f16(scale) RNE, 16 bytes (value j in the
+//         low nibble of byte j, value j + 16 in its high nibble).
+// The f32 arithmetic is IEEE (correctly rounded division and sqrt).
+//
+// Layout on CDNA: one 256-thread workgroup per token.  Thread t owns values
+// t + 256p of the K and V rows; a 32-value block is exactly half a
+// wavefront, so block maxima are half-wave reductions (DPP steps and one
+// ds_swizzle) and the Q4_0 nibble pairing is an xor-16 swizzle.  The V sum
+// of squares folds in order from LDS on one lane.
+#include "device_common.hpp"
+#include "launch.hpp"
+
+namespace atlas {
+namespace {
+
+constexpr uint32_t kThreads = 256;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Exchange with lane ^ 16 inside each 32-lane half (ds_swizzle bit mode:
+// and_mask 0x1f, xor_mask 0x10).
+__device__ __forceinline__ int swap16(int v) { return __builtin_amdgcn_ds_swizzle(v, 0x401f); }
+
+// Maximum over each 32-lane half: four DPP steps inside 16-lane rows
+// (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), then one swizzle.
+// fmaxf ignores NaN lanes, as the reference's max fold does.
+__device__ __forceinline__ float half_wave_max(float v) {
+    v = fmaxf(v, dpp_f32<0xb1>(v));
+    v = fmaxf(v, dpp_f32<0x4e>(v));
+    v = fmaxf(v, dpp_f32<0x141>(v));
+    v = fmaxf(v, dpp_f32<0x140>(v));
+    return fmaxf(v, __int_as_float(swap16(__float_as_int(v))));
+}
+
+__device__ __forceinline__ uint32_t f16_bits(float v) { return f2h(v); }
+
+// Store one encoded block.  Lanes of a half wave hold the block's 32 values
+// (lane % 32 = index in the block); dst points at the block's first byte.
+template <int FMT>
+__device__ __forceinline__ void encode_block(float v, uint8_t* dst, uint32_t j) {
+    const float amax = half_wave_max(__builtin_fabsf(v));
+    if (FMT == kKvQ8_0) {
+        const float scale = amax == 0.0f ? 0.0f : fdiv_rn(amax, 127.0f);
+        if (j == 0) {
+            dst[0] = static_cast<uint8_t>(f16_bits(scale));
+            dst[1] = static_cast<uint8_t>(f16_bits(scale) >> 8);
+        }
+        int code = 0;
+        if (scale != 0.0f) code = static_cast<int>(roundf(fminf(fmaxf(fdiv_rn(v, scale), -127.0f), 127.0f)));
+        dst[2 + j] = static_cast<uint8_t>(static_cast<int8_t>(code));
+    } else {
+        // signed maximum: the first lane (lowest index) of each half whose |v|
+        // equals that half's maximum; both halves are read with scalar readlanes
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(amax > 0.0f && __builtin_fabsf(v) == amax);
+        const uint32_t lo = static_cast<uint32_t>(hit), hi = static_cast<uint32_t>(hit >> 32);
+        const float s_lo = readlane_f32(v, lo ? static_cast<uint32_t>(__builtin_ctz(lo)) : 0u);
+        const float s_hi = readlane_f32(v, hi ? 32u + static_cast<uint32_t>(__builtin_ctz(hi)) : 32u);
+        const float smax = (__lane_id() & 32u) ? s_hi : s_lo;
+        const float scale = amax == 0.0f ? 0.0f : fdiv_rn(smax, -8.0f);
+        int code = 0;
+        if (scale != 0.0f) {
+            const float t = fdiv_rn(v, scale) + 8.5f;
+            code = t >= 15.0f ? 15 : (t > 0.0f ? static_cast<int>(t) : 0);
+        }
+        const int high = swap16(code);  // lane j < 16 receives the code of value j + 16
+        if (j == 0) {
+            dst[0] = static_cast<uint8_t>(f16_bits(scale));
+            dst[1] = static_cast<uint8_t>(f16_bits(scale) >> 8);
+        }
+        if (j < 16) dst[2 + j] = static_cast<uint8_t>(code | (high << 4));
+    }
+}
+
+// P: values per thread and row (kv_width <= 256 * P).
+template <int FMT, bool VNORM, int P>
+__global__ __launch_bounds__(256) void kv_append_kernel(KvAppendArgs a) {
+    extern __shared__ __align__(16) float sq[];  // kv_width squares of V (VNORM)
+    __shared__ float inv_shared;
+    const uint32_t t = blockIdx.x, tid = threadIdx.x;
+    const uint32_t position = a.positions[t];
+    if (position >= a.capacity) return;  // workgroup-uniform
+    const uint32_t w = a.kv_width;
+    const float* key = a.key + static_cast<size_t>(t) * w;
+    const float* value = a.value + static_cast<size_t>(t) * w;
+    const uint32_t passes = (w + kThreads - 1) / kThreads;
+
+    float k[P], v[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const uint32_t i = tid + kThreads * p;
+        const bool in = p < static_cast<int>(passes) && i < w;
+        k[p] = in ? key[i] : 0.0f;
+        v[p] = in ? value[i] : 0.0f;
+    }
+    if (VNORM) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const uint32_t i = tid + kThreads * p;
+            if (p < static_cast<int>(passes) && i < w) sq[i] = v[p] * v[p];
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float s = 0.0f;
+            const f32x4* row = reinterpret_cast<const f32x4*>(sq);
+            for (uint32_t c = 0; c < w / 4; c += 64) s = fold_lds_chunk(row + c, min(64u, w / 4 - c), s);
+            inv_shared = inverse_rms(s, static_cast<float>(w), a.epsilon);
+        }
+        __syncthreads();
+        const float inv = inv_shared;
+#pragma unroll
+        for (int p = 0; p < P; ++p) v[p] = v[p] * inv;
+    }
+
+    const size_t half = static_cast<size_t>(a.capacity);  // rows per cache half
+    if (FMT == kKvF32) {
+        float* kc = reinterpret_cast<float*>(a.cache) + static_cast<size_t>(position) * w;
+        float* vc = reinterpret_cast<float*>(a.cache) + (half + position) * w;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const uint32_t i = tid + kThreads * p;
+            if (p < static_cast<int>(passes) && i < w) {
+                kc[i] = k[p];
+                vc[i] = v[p];
+            }
+        }
+    } else {
+        constexpr uint32_t kBlock = FMT == kKvQ8_0 ? 34 : 18;
+        const uint32_t blocks = w / 32;
+        uint8_t* kc = a.cache + static_cast<size_t>(position) * blocks * kBlock;
+        uint8_t* vc = a.cache + (half + position) * blocks * kBlock;
+        const uint32_t j = tid & 31u;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            if (p >= static_cast<int>(passes)) break;  // workgroup-uniform
+            // kv_width % 32 == 0, so a half wave is all in or all out; every
+            // cross-lane step of the encoder stays inside its half (DPP rows,
+            // xor-16 swizzle, the half's own readlane), so an inactive half
+            // does not affect an active one
+            const uint32_t b = (tid + kThreads * p) / 32;
+            if (b < blocks) {
+                encode_block<FMT>(k[p], kc + b * kBlock, j);
+                encode_block<FMT>(v[p], vc + b * kBlock, j);
+            }
+        }
+    }
+}
+
+template <int FMT, int P>
+hipError_t launch_p(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
+    if (vnorm)
+        hipLaunchKernelGGL((kv_append_kernel<FMT, true, P>), dim3(a.tokens), dim3(kThreads),
+                           a.kv_width * sizeof(float), stream, a);
+    else
+        hipLaunchKernelGGL((kv_append_kernel<FMT, false, P>), dim3(a.tokens), dim3(kThreads), 0, stream, a);
+    return hipGetLastError();
+}
+
+// Registers scale with the values per thread, so the row width picks the
+// instantiation (256 -> 1 value per thread and row, 4096 -> 16).
+template <int FMT>
+hipError_t launch_fmt(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
+    const uint32_t p = (a.kv_width + kThreads - 1) / kThreads;
+    if (p <= 1) return launch_p<FMT, 1>(stream, a, vnorm);
+    if (p <= 2) return launch_p<FMT, 2>(stream, a, vnorm);
+    if (p <= 4) return launch_p<FMT, 4>(stream, a, vnorm);
+    if (p <= 8) return launch_p<FMT, 8>(stream, a, vnorm);
+    return launch_p<FMT, 16>(stream, a, vnorm);
+}
+
+}  // namespace
+
+hipError_t launch_kv_append(hipStream_t stream, int format, bool vnorm, const KvAppendArgs& a) {
+    switch (format) {
+        case kKvF32: return launch_fmt<kKvF32>(stream, a, vnorm);
+        case kKvQ8_0: return launch_fmt<kKvQ8_0>(stream, a, vnorm);
+        case kKvQ4_0: return launch_fmt<kKvQ4_0>(stream, a, vnorm);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace atlas

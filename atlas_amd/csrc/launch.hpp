@@ -108,4 +108,18 @@ struct MatvecArgs {
 uint32_t q4_0_matvec_max_input();
 hipError_t launch_q4_0_matvec(hipStream_t stream, MatvecArgs a);
 
+// KV-cache append with optional fused V RMSNorm (kv_kernels.hip).
+enum KvFormat : int { kKvF32 = 0, kKvQ8_0 = 1, kKvQ4_0 = 2 };
+struct KvAppendArgs {
+    const float* key;           // [tokens, kv_width]
+    const float* value;         // [tokens, kv_width]
+    uint8_t* cache;             // [K | V][capacity][row]
+    const uint32_t* positions;  // [tokens] cache position of each token (device)
+    uint32_t kv_width;          // <= 4096; multiple of 32 for Q8_0/Q4_0
+    uint32_t capacity;
+    uint32_t tokens;
+    float epsilon;
+};
+hipError_t launch_kv_append(hipStream_t stream, int format, bool vnorm, const KvAppendArgs& a);
+
 }  // namespace atlas

@@ -279,6 +279,14 @@ class HipRuntime:
                                                                _ptr(q_out), _ptr(k_out), _ptr(v_out), input_width,
                                                                q_width, kv_width, _ptr(rms_weight), eps))
 
+    # KV-cache append with the fused V RMSNorm (kv_append_decode_*[_batch|_vnorm],
+    # kernels.metal:1197-1436); fmt is "f32", "q8_0" or "q4_0".
+    def kv_append(self, fmt, key, value, cache, kv_width, capacity, positions, tokens, vnorm, eps):
+        fn = {"f32": self.lib.atlas_hip_kv_append_f32, "q8_0": self.lib.atlas_hip_kv_append_q8_0,
+              "q4_0": self.lib.atlas_hip_kv_append_q4_0}[fmt]
+        self._check(fn(self.ctx, _ptr(key), _ptr(value), _ptr(cache), kv_width, capacity, _ptr(positions), tokens,
+                       1 if vnorm else 0, eps))
+
     def matmul_q4_0_gate_up_rms(self, x, gw, uw, g_out, u_out, input_width, output_width, rms_weight, eps):
         self._check(self.lib.atlas_hip_matmul_q4_0_gate_up_rms_f32(self.ctx, _ptr(x), _ptr(gw), _ptr(uw), _ptr(g_out),
                                                                    _ptr(u_out), input_width, output_width,

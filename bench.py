@@ -129,7 +129,8 @@ class ConfigOps(Ops):
     """Per-op timing at the other op configurations (separate lines, not the headline):
     c1 = BASELINE configs[0] (SmolLM2-135M-shaped FP32 ops, T=128),
     c2 = BASELINE configs[1] (SmolLM2-1.7B-shaped FP16 storage, T=2048),
-    gemv = the RMS-folded Q4_0 decode projections of one Gemma-4-E2B-like token."""
+    gemv = the RMS-folded Q4_0 decode projections of one Gemma-4-E2B-like token,
+    kv = the KV append with the fused V RMSNorm (prefill batch and one decode token)."""
 
     def __init__(self, wl, rope_tables, cfg):
         r = wl.rng(2025)
@@ -177,6 +178,26 @@ class ConfigOps(Ops):
                                 lambda rt, s: rt.matmul_q4_0_gate_up_rms(s["x"], s["gw"], s["uw"], s["go"], s["uo"],
                                                                          H, F, s["w"], eps)),
             }
+        elif cfg == "kv":
+            # KV append with the fused V RMSNorm at the
+            # Gemma-4-E2B-like shape (one KV head of 256): a 4096-token prefill
+            # batch into a 4096-position cache, and one decode token
+            L = wl.GemmaLayerShape()
+            T, W, cap = L.tokens, L.head_dim, L.tokens
+            self.tokens = T
+            self.host = {"k": wl.normal(r, T * W), "v": wl.normal(r, T * W),
+                         "pos": np.arange(T, dtype=np.uint32), "pos1": np.array([T // 2], np.uint32)}
+            rows = {"f32": W * 4, "q8_0": W // 32 * 34, "q4_0": W // 32 * 18}
+            self.table = {}
+            for fmt in ("f32", "q8_0", "q4_0"):
+                cache_f = 2 * cap * rows[fmt] // 4
+                self.table[f"kv_append_{fmt}_vnorm_T{T}"] = (
+                    ["k", "v", "pos"], {f"c_{fmt}": cache_f}, 2 * T * W * 4 + T * 4 + 2 * T * rows[fmt],
+                    (lambda f: lambda rt, s: rt.kv_append(f, s["k"], s["v"], s[f"c_{f}"], W, cap, s["pos"], T,
+                                                          True, L.eps))(fmt))
+            self.table["kv_append_q4_0_vnorm_decode"] = (
+                ["k", "v", "pos1"], {"c1": 2 * cap * rows["q4_0"] // 4}, 2 * W * 4 + 4 + 2 * rows["q4_0"],
+                lambda rt, s: rt.kv_append("q4_0", s["k"], s["v"], s["c1"], W, cap, s["pos1"], 1, True, L.eps))
         else:
             S = wl.SmolShape()
             T, H, QH, KH, D, F, V = S.tokens, S.hidden, S.q_heads, S.kv_heads, S.head_dim, S.ffn, S.vocab
@@ -324,9 +345,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma-separated op subset: per-op timing only (profiling)")
     ap.add_argument("--copy-mib", type=int, default=0, help="also time a device-to-device copy of this size")
-    ap.add_argument("--config", choices=["c3c4", "c1", "c2", "gemv"], default="c3c4",
+    ap.add_argument("--config", choices=["c3c4", "c1", "c2", "gemv", "kv"], default="c3c4",
                     help="c1 / c2: per-op lines for BASELINE configs[0] / configs[1]; gemv: the RMS-folded "
-                         "Q4_0 decode projections of one token -- instead of the headline")
+                         "Q4_0 decode projections of one token; kv: the KV append with the fused V norm "
+                         "-- instead of the headline")
     ap.add_argument("--decode", action="store_true",
                     help="BASELINE configs[4] batched decode (per-layer latency, eager and HIP graph) instead")
     args = ap.parse_args()
@@ -352,7 +374,7 @@ def main():
         for name, (_, _, nbytes, launch) in cops.table.items():
             # the weight-streaming projections need >= 1 GiB of distinct weights
             # to keep the 256 MB MALL out of the measurement
-            cap = 1024 if args.config == "gemv" else 64
+            cap = 1024 if args.config in ("gemv", "kv") else 64
             nsets = min(cap, max(4, math.ceil(ROTATION_BYTES / cops.set_bytes(name))))
             log(f"timing {args.config} {name} ({nsets} rotating sets)")
             sets = cops.build_sets(rt, [name], nsets)

@@ -301,6 +301,29 @@ int atlas_hip_matmul_q4_0_gate_up_rms_f32(atlas_hip_ctx *ctx, const float *input
                                           float *gate_output, float *up_output, uint32_t input_width,
                                           uint32_t output_width, const float *rms_weight, float epsilon);
 
+/* ---- KV-cache append with the fused V RMSNorm and Q8_0/Q4_0 encoders ----- */
+
+/* kv_append_decode_{f32,q8_0,q4_0}[_batch|_vnorm] (kernels.metal:1197-1436;
+ * callers gemma4_executor.rs:3826-3850 prefill, :4326-4368 decode).
+ * key/value: [tokens, kv_width] f32; positions: [tokens] device u32 (decode:
+ * tokens = 1 and the position buffer); tokens whose position is >= capacity
+ * are skipped.  cache layout [K | V][capacity][row]: a row is kv_width f32
+ * (f32) or kv_width/32 blocks of 34 (Q8_0) / 18 (Q4_0) bytes.  vnorm != 0
+ * scales each V row by 1 / sqrt(sum v^2 / kv_width + epsilon) (sum in index
+ * order: rms_norm_groups_in_place_unweighted_f32, kernels.metal:919-929)
+ * before it is stored; the value buffer is not modified.  kv_width <= 4096,
+ * a multiple of 4 (f32) or 32 (Q8_0, Q4_0).  Bit-exact against the CPU
+ * restatement of the Metal encoders (IEEE division and sqrt). */
+int atlas_hip_kv_append_f32(atlas_hip_ctx *ctx, const float *key, const float *value, float *cache,
+                            uint32_t kv_width, uint32_t capacity, const uint32_t *positions,
+                            uint32_t tokens, int vnorm, float epsilon);
+int atlas_hip_kv_append_q8_0(atlas_hip_ctx *ctx, const float *key, const float *value, uint8_t *cache,
+                             uint32_t kv_width, uint32_t capacity, const uint32_t *positions,
+                             uint32_t tokens, int vnorm, float epsilon);
+int atlas_hip_kv_append_q4_0(atlas_hip_ctx *ctx, const float *key, const float *value, uint8_t *cache,
+                             uint32_t kv_width, uint32_t capacity, const uint32_t *positions,
+                             uint32_t tokens, int vnorm, float epsilon);
+
 /* ---- host-slice operator API (atlas_ops::NeuralOps) --------------------- */
 
 /* NeuralOps::embedding -> MetalRuntime::embedding_lookup (lib.rs:1393-1433). */

@@ -703,3 +703,100 @@ void oracle_matvec_q4_0_rms_f64(const float *input, const uint8_t *weights, cons
     }
 }
 
+/* ======================================================================== */
+/* KV-cache append, fused V RMSNorm, Q8_0 / Q4_0 encoders                   */
+/* ======================================================================== */
+
+/* Restates kv_append_decode_{f32,q8_0,q4_0}[_batch] (crates/atlas-metal/src/
+ * kernels.metal:1197-1344) and the unfused V norm
+ * rms_norm_groups_in_place_unweighted_f32 (:919-929) that the _vnorm
+ * kernels fold in (:1346-1436): inv = 1 / sqrt(sum v^2 / width + eps) with
+ * the sum in index order (IEEE sqrt and division; Metal's rsqrt cannot be
+ * reproduced off Apple hardware), v' = v * inv. */
+static float kv_inv_rms(const float *v, size_t width, float epsilon) {
+    float s = 0.0f;
+    for (size_t i = 0; i < width; ++i) s = s + v[i] * v[i];
+    return 1.0f / sqrtf(s / (float)width + epsilon);
+}
+
+/* Q8_0 block (kv_append_decode_q8_0, kernels.metal:1222-1231): m = max|v|,
+ * scale = m == 0 ? 0 : m / 127, code = round-half-away(clamp(v / scale,
+ * -127, 127)), f16 scale with IEEE RNE. */
+void oracle_encode_q8_0_block(const float *v, uint8_t *out34) {
+    float maximum = 0.0f;
+    for (int i = 0; i < 32; ++i) maximum = fmaxf(maximum, fabsf(v[i]));
+    const float scale = maximum == 0.0f ? 0.0f : maximum / 127.0f;
+    const uint16_t bits = oracle_f32_to_f16_rne(scale);
+    out34[0] = (uint8_t)bits;
+    out34[1] = (uint8_t)(bits >> 8);
+    for (int i = 0; i < 32; ++i) {
+        int code = 0;
+        if (scale != 0.0f) code = (int)roundf(fminf(fmaxf(v[i] / scale, -127.0f), 127.0f));
+        out34[2 + i] = (uint8_t)(int8_t)code;
+    }
+}
+
+/* Q4_0 block (kv_append_decode_q4_0, kernels.metal:1247-1256): the first
+ * value with the largest |v| (strictly greater replaces) is the signed
+ * maximum s, scale = s / -8, code = clamp(trunc(v / scale + 8.5), 0, 15)
+ * (NaN -> 0), byte j = code_j | code_{j+16} << 4, f16 scale with IEEE RNE. */
+static int q4_code(float v, float scale) {
+    if (scale == 0.0f) return 0;
+    const float t = v / scale + 8.5f;
+    if (t >= 15.0f) return 15;
+    if (t > 0.0f) return (int)t;
+    return 0;
+}
+
+void oracle_encode_q4_0_block(const float *v, uint8_t *out18) {
+    float maximum = 0.0f, signed_maximum = 0.0f;
+    for (int i = 0; i < 32; ++i) {
+        if (fabsf(v[i]) > maximum) {
+            maximum = fabsf(v[i]);
+            signed_maximum = v[i];
+        }
+    }
+    const float scale = maximum == 0.0f ? 0.0f : signed_maximum / -8.0f;
+    const uint16_t bits = oracle_f32_to_f16_rne(scale);
+    out18[0] = (uint8_t)bits;
+    out18[1] = (uint8_t)(bits >> 8);
+    for (int i = 0; i < 16; ++i)
+        out18[2 + i] = (uint8_t)(q4_code(v[i], scale) | (q4_code(v[i + 16], scale) << 4));
+}
+
+/* format: 0 f32, 1 Q8_0, 2 Q4_0.  Tokens with positions[t] >= capacity are
+ * skipped; the value input is not modified. */
+void oracle_kv_append(int format, const float *key, const float *value, uint8_t *cache, size_t kv_width,
+                      size_t capacity, const uint32_t *positions, size_t tokens, int vnorm, float epsilon) {
+    float v[4096];
+    if (kv_width > 4096) return;
+    const size_t row = format == 0 ? kv_width * 4 : (kv_width / 32) * (format == 1 ? 34 : 18);
+    for (size_t t = 0; t < tokens; ++t) {
+        const size_t position = positions[t];
+        if (position >= capacity) continue;
+        const float *k = key + t * kv_width;
+        memcpy(v, value + t * kv_width, kv_width * sizeof(float));
+        if (vnorm) {
+            const float inv = kv_inv_rms(v, kv_width, epsilon);
+            for (size_t i = 0; i < kv_width; ++i) v[i] = v[i] * inv;
+        }
+        uint8_t *kc = cache + position * row;
+        uint8_t *vc = cache + (capacity + position) * row;
+        if (format == 0) {
+            memcpy(kc, k, kv_width * sizeof(float));
+            memcpy(vc, v, kv_width * sizeof(float));
+        } else {
+            const size_t bytes = format == 1 ? 34 : 18;
+            for (size_t b = 0; b < kv_width / 32; ++b) {
+                if (format == 1) {
+                    oracle_encode_q8_0_block(k + 32 * b, kc + bytes * b);
+                    oracle_encode_q8_0_block(v + 32 * b, vc + bytes * b);
+                } else {
+                    oracle_encode_q4_0_block(k + 32 * b, kc + bytes * b);
+                    oracle_encode_q4_0_block(v + 32 * b, vc + bytes * b);
+                }
+            }
+        }
+    }
+}
+

@@ -151,6 +151,13 @@ void oracle_matvec_q4_0_rms_f64(const float *input, const uint8_t *weights, cons
                                 size_t input_width, size_t output_width, float epsilon, double *output,
                                 double *magnitude);
 
+/* KV-cache append with the fused V RMSNorm and the Q8_0 / Q4_0 encoders
+ * (kernels.metal:919-929, 1197-1436).  format: 0 f32, 1 Q8_0, 2 Q4_0. */
+void oracle_encode_q8_0_block(const float *v, uint8_t *out34);
+void oracle_encode_q4_0_block(const float *v, uint8_t *out18);
+void oracle_kv_append(int format, const float *key, const float *value, uint8_t *cache, size_t kv_width,
+                      size_t capacity, const uint32_t *positions, size_t tokens, int vnorm, float epsilon);
+
 #ifdef __cplusplus
 }
 #endif

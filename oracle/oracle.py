@@ -60,6 +60,9 @@ _SIGS = {
     "oracle_combine_ple": ([P, P, P, SZ], None),
     "oracle_matvec_q4_0_rms_ref": ([P, P, P, SZ, SZ, F, P], None),
     "oracle_matvec_q4_0_rms_f64": ([P, P, P, SZ, SZ, F, P, P], None),
+    "oracle_encode_q8_0_block": ([P, P], None),
+    "oracle_encode_q4_0_block": ([P, P], None),
+    "oracle_kv_append": ([c_int, P, P, P, SZ, SZ, P, SZ, c_int, F], None),
     "oracle_add_f32": ([P, P, P, SZ], None),
     "oracle_multiply_f32": ([P, P, P, SZ], None),
     "oracle_scale_f32": ([P, F, P, SZ], None),
@@ -353,4 +356,33 @@ def matvec_q4_0_rms_f64(x, weights, rms_weight, input_width, output_width, eps):
     lib().oracle_matvec_q4_0_rms_f64(_p(xx), _p(ww), None if rw is None else _p(rw), input_width, output_width, eps,
                                      _p(out), _p(mag))
     return out, mag
+
+
+KV_FORMATS = {"f32": 0, "q8_0": 1, "q4_0": 2}
+KV_BLOCK_BYTES = {"q8_0": 34, "q4_0": 18}
+
+
+def kv_row_bytes(fmt, kv_width):
+    return kv_width * 4 if fmt == "f32" else (kv_width // 32) * KV_BLOCK_BYTES[fmt]
+
+
+def kv_append(fmt, key, value, cache, kv_width, capacity, positions, vnorm, eps):
+    """kv_append_decode_*[_batch|_vnorm] restated; returns the updated cache bytes."""
+    k, v, pos = _c(key, f32), _c(value, f32), _c(positions, u32)
+    out = np.array(cache, u8, copy=True)
+    lib().oracle_kv_append(KV_FORMATS[fmt], _p(k), _p(v), _p(out), kv_width, capacity, _p(pos), pos.size,
+                           1 if vnorm else 0, eps)
+    return out
+
+
+def encode_q8_0_block(values):
+    v, out = _c(values, f32), np.zeros(34, u8)
+    lib().oracle_encode_q8_0_block(_p(v), _p(out))
+    return out
+
+
+def encode_q4_0_block(values):
+    v, out = _c(values, f32), np.zeros(18, u8)
+    lib().oracle_encode_q4_0_block(_p(v), _p(out))
+    return out
 

@@ -450,3 +450,108 @@ def test_reference_matvec_generators():
         for j in range(16):
             nib = (i * 7 + j * 13) % 16
             assert W[i, 2 + j] == nib | (nib << 4)
+
+
+# ------------------------------------------- KV append: Q8_0 / Q4_0 encoders
+
+def _np_encode_q8_0(v):
+    """Independent vectorised restatement of kv_append_decode_q8_0's block encoder
+    (kernels.metal:1222-1231) in float32 numpy: [n, 32] -> [n, 34] bytes."""
+    v = v.astype(f32)
+    m = np.max(np.abs(v), axis=1)
+    scale = np.where(m == 0, f32(0), m / f32(127)).astype(f32)
+    safe = np.where(scale == 0, f32(1), scale)
+    q = np.clip(v / safe[:, None], f32(-127), f32(127))
+    code = np.where(scale[:, None] == 0, 0, np.sign(q) * np.floor(np.abs(q) + 0.5)).astype(np.int8)
+    out = np.zeros((v.shape[0], 34), np.uint8)
+    out[:, 0:2] = scale.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = code.view(np.uint8)
+    return out
+
+
+def _np_encode_q4_0(v):
+    """kv_append_decode_q4_0's block encoder (kernels.metal:1247-1256): the first
+    index of the largest |v| gives the signed maximum."""
+    v = v.astype(f32)
+    first = np.argmax(np.abs(v), axis=1)             # argmax returns the first occurrence
+    smax = v[np.arange(v.shape[0]), first]
+    m = np.abs(smax)
+    scale = np.where(m == 0, f32(0), smax / f32(-8)).astype(f32)
+    safe = np.where(scale == 0, f32(1), scale)
+    t = (v / safe[:, None]).astype(f32) + f32(8.5)
+    code = np.where(t >= 15, 15, np.where(t > 0, np.trunc(t), 0)).astype(np.int64)
+    code[scale == 0] = 0
+    out = np.zeros((v.shape[0], 18), np.uint8)
+    out[:, 0:2] = scale.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = (code[:, :16] | (code[:, 16:] << 4)).astype(np.uint8)
+    return out
+
+
+def _adversarial_blocks(r):
+    blocks = [r.standard_normal(32), np.zeros(32), (r.integers(-20, 20, 32) / 4.0),   # exact halves: rounding ties
+              np.full(32, -3.0), np.where(np.arange(32) % 2 == 0, 2.5, -2.5),          # |max| tie, signs differ
+              r.standard_normal(32) * 1e30, r.standard_normal(32) * 1e-30, np.arange(32) - 16.0]
+    b = np.array(blocks, f32)
+    b[3, 5] = 3.0                                          # equal |max| with the opposite sign later
+    return b
+
+
+def test_kv_encoders_pinned(ora):
+    """The C encoders equal an independent numpy restatement on random and
+    adversarial blocks, and satisfy the reference's own round-trip KAT
+    (phase_11a_gguf.rs:33-55: values (i-16)/7, |v - deq| <= 0.35 Q4_0, 0.03 Q8_0)."""
+    r = np.random.default_rng(41)
+    v = np.concatenate([r.standard_normal((500, 32)).astype(f32) * f32(3), _adversarial_blocks(r)])
+    got8 = np.array([ora.encode_q8_0_block(b) for b in v])
+    got4 = np.array([ora.encode_q4_0_block(b) for b in v])
+    assert np.array_equal(got8, _np_encode_q8_0(v))
+    assert np.array_equal(got4, _np_encode_q4_0(v))
+    kat = ((np.arange(32) - 16.0) / 7.0).astype(f32)
+    dq4 = ora.dequant_q4_0_block(ora.encode_q4_0_block(kat))
+    assert np.all(np.abs(dq4 - kat) <= 0.35)
+    b8 = ora.encode_q8_0_block(kat)
+    d8 = np.frombuffer(b8[:2].tobytes(), np.float16).astype(np.float64)[0]
+    dq8 = b8[2:].view(np.int8).astype(np.float64) * d8
+    assert np.all(np.abs(dq8 - kat) <= 0.03)
+
+
+def test_kv_encoder_error_bounds(ora):
+    """Round trip of random blocks within half a step plus the f16 scale rounding;
+    the block maximum maps to code -127/127 (Q8_0) and to code 0 (Q4_0)."""
+    r = np.random.default_rng(43)
+    for _ in range(300):
+        v = (r.standard_normal(32) * r.uniform(0.01, 100)).astype(f32)
+        b8 = ora.encode_q8_0_block(v)
+        s = float(np.max(np.abs(v))) / 127.0
+        d = float(np.frombuffer(b8[:2].tobytes(), np.float16)[0])
+        codes = b8[2:].view(np.int8).astype(np.float64)
+        assert np.all(np.abs(codes * d - v) <= s / 2 + 127 * abs(d - s) + 1e-6 * s)
+        assert abs(codes[np.argmax(np.abs(v))]) == 127
+        b4 = ora.encode_q4_0_block(v)
+        dq = ora.dequant_q4_0_block(b4).astype(np.float64)
+        s4 = abs(float(v[np.argmax(np.abs(v))])) / 8.0
+        d4 = abs(float(np.frombuffer(b4[:2].tobytes(), np.float16)[0]))
+        # codes clamp at 15 (value +7 * scale): the positive side of a negative
+        # signed maximum saturates, so bound only the unclamped values
+        ok = np.abs(v.astype(np.float64)) <= 7 * s4
+        assert np.all(np.abs(dq - v)[ok] <= s4 / 2 + 8 * abs(d4 - s4) + 1e-6 * s4)
+
+
+def test_kv_append_layout_and_vnorm(ora):
+    """Cache rows land at [K | V][position]; positions >= capacity are skipped;
+    the V norm scales each row by 1/sqrt(mean v^2 + eps) (float64 check)."""
+    r = np.random.default_rng(47)
+    w, cap, T = 64, 6, 5
+    key, value = r.standard_normal((T, w)).astype(f32), r.standard_normal((T, w)).astype(f32)
+    pos = np.array([4, 0, 9, 2, 6], np.uint32)     # 9 and 6 are outside the cache
+    cache = np.full(2 * cap * w * 4, 0xAB, np.uint8)
+    out = ora.kv_append("f32", key, value, cache, w, cap, pos, True, 1e-6).view(f32).reshape(2, cap, w)
+    for t, p in enumerate(pos):
+        if p >= cap:
+            continue
+        assert np.array_equal(out[0, p], key[t])
+        inv = 1.0 / np.sqrt(np.mean(value[t].astype(np.float64) ** 2) + 1e-6)
+        np.testing.assert_allclose(out[1, p], value[t] * inv, rtol=2e-6)
+    untouched = [1, 3, 5]
+    raw = cache.view(f32).reshape(2, cap, w)
+    assert np.array_equal(out[:, untouched].view(np.uint32), raw[:, untouched].view(np.uint32))
