@@ -635,7 +635,7 @@ static int ple(atlas_hip_ctx* ctx, int q6, const uint8_t* table, const uint32_t*
 
 static int q4_matvec(atlas_hip_ctx* ctx, const float* input, const float* rms_weight, float epsilon,
                      uint32_t input_width, uint32_t segments, const uint8_t* const* weights, float* const* outputs,
-                     const uint32_t* widths, const char* op) {
+                     const uint32_t* widths, const char* op, const float* ple = nullptr, uint32_t ple_offset = 0) {
     int rc = enter(ctx);
     if (rc) return rc;
     if (!input) return invalid(ctx, "matvec input is null");
@@ -650,6 +650,8 @@ static int q4_matvec(atlas_hip_ctx* ctx, const float* input, const float* rms_we
     a.epsilon = epsilon;
     a.input_width = input_width;
     a.segments = segments;
+    a.ple = ple;
+    a.ple_offset = ple_offset;
     for (uint32_t i = 0; i < segments; ++i) {
         if (!weights[i] || !outputs[i]) return invalid(ctx, "matvec weights/output is null");
         if (reinterpret_cast<uintptr_t>(weights[i]) & 1) return invalid(ctx, "Q4_0 weights must be 2-byte aligned");
@@ -659,6 +661,17 @@ static int q4_matvec(atlas_hip_ctx* ctx, const float* input, const float* rms_we
         a.width[i] = widths[i];
     }
     return launched(ctx, atlas::launch_q4_0_matvec(ctx->stream, a), op);
+}
+
+int atlas_hip_ple_gate_gelu_f32(atlas_hip_ctx* ctx, const float* input, const uint8_t* weights, const float* ple,
+                                uint32_t ple_offset, float* output, uint32_t input_width, uint32_t output_width) {
+    int rc = enter(ctx);
+    if (rc) return rc;
+    if (!ple) return invalid(ctx, "PLE buffer is null");
+    const uint8_t* w[1] = {weights};
+    float* o[1] = {output};
+    const uint32_t n[1] = {output_width};
+    return q4_matvec(ctx, input, nullptr, 0.0f, input_width, 1, w, o, n, "ple_gate_gelu", ple, ple_offset);
 }
 
 int atlas_hip_matvec_q4_0_rms_f32(atlas_hip_ctx* ctx, const float* input, const uint8_t* weights, float* output,

@@ -97,6 +97,10 @@ hipError_t launch_ple_quant(hipStream_t stream, int q6k, const uint8_t* table, c
 struct MatvecArgs {
     const float* input;
     const float* rms_weight;
+    // epilogue: out = gelu_tanh(total) * ple[ple_offset + row] when ple is set
+    // (the PLE input gate); otherwise out = total (* inv_rms with rms_weight)
+    const float* ple;
+    uint32_t ple_offset;
     float epsilon;
     uint32_t input_width;  // multiple of 32, <= q4_0_matvec_max_input()
     uint32_t segments;     // 1..3

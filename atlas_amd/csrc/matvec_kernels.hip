@@ -4,6 +4,8 @@
 //   matvec_q4_0_16row_mv_rms           :3786-3864  one projection
 //   matmul_q4_0_qkv_16row_mv_rms       :3368-3467  Q, K and V in one dispatch
 //   matmul_q4_0_gate_up_16row_mv_rms   :3468-3564  gate and up in one dispatch
+//   gemma4_ple_gate_gelu_f32           :803-881    the PLE input gate: plain
+//       matvec, then gelu(gate) * ple[ple_offset + row] (kernels.metal:773-801)
 //   callers crates/atlas-model/src/gemma4_executor.rs:2082-2119, 2502-2612
 //
 // One decode token: output[o] = inv_rms(x) * sum_k (x_k * w_k) * deq(W[o, k]),
@@ -229,7 +231,12 @@ __global__ __launch_bounds__(256) void q4_0_matvec_kernel(MatvecArgs a) {
         }
     }
     const float total = group_sum<LPR>(acc);
-    if (s == 0 && g < wrows) out[row0 + row] = rms ? total * inv : total;
+    if (s == 0 && g < wrows) {
+        if (a.ple)  // PLE input gate: GELU of the projection times the layer's PLE slice
+            out[row0 + row] = gelu_tanh_f32(total) * a.ple[a.ple_offset + row0 + row];
+        else
+            out[row0 + row] = rms ? total * inv : total;
+    }
 }
 
 template <int LPR, int NBT>

@@ -279,6 +279,11 @@ class HipRuntime:
                                                                _ptr(q_out), _ptr(k_out), _ptr(v_out), input_width,
                                                                q_width, kv_width, _ptr(rms_weight), eps))
 
+    # PLE input gate: gelu(Q4_0 matvec) * PLE slice (gemma4_ple_gate_gelu_f32, kernels.metal:803-881)
+    def ple_gate_gelu(self, x, weights, ple, ple_offset, out, input_width, output_width):
+        self._check(self.lib.atlas_hip_ple_gate_gelu_f32(self.ctx, _ptr(x), _ptr(weights), _ptr(ple), ple_offset,
+                                                         _ptr(out), input_width, output_width))
+
     # KV-cache append with the fused V RMSNorm (kv_append_decode_*[_batch|_vnorm],
     # kernels.metal:1197-1436); fmt is "f32", "q8_0" or "q4_0".
     def kv_append(self, fmt, key, value, cache, kv_width, capacity, positions, tokens, vnorm, eps):

@@ -301,6 +301,18 @@ int atlas_hip_matmul_q4_0_gate_up_rms_f32(atlas_hip_ctx *ctx, const float *input
                                           float *gate_output, float *up_output, uint32_t input_width,
                                           uint32_t output_width, const float *rms_weight, float epsilon);
 
+/* gemma4_ple_gate_gelu_f32 (kernels.metal:803-881; the fused form of
+ * matvec_q4_0_16row_mv + ple_gelu_multiply_offset_f32, caller
+ * gemma4_executor.rs:4063-4081): the PLE input gate of one decode token,
+ * output[o] = gelu_tanh(sum_k input[k] * deq(W[o, k])) * ple[ple_offset + o],
+ * with the reference's GELU (kernels.metal:752-767).  W as above
+ * ([output_width, input_width] Q4_0, input_width % 32 == 0, <= 4096); the
+ * projection is floating point (tolerance parity), the GELU and the product
+ * are the reference's roundings. */
+int atlas_hip_ple_gate_gelu_f32(atlas_hip_ctx *ctx, const float *input, const uint8_t *weights,
+                                const float *ple, uint32_t ple_offset, float *output, uint32_t input_width,
+                                uint32_t output_width);
+
 /* ---- KV-cache append with the fused V RMSNorm and Q8_0/Q4_0 encoders ----- */
 
 /* kv_append_decode_{f32,q8_0,q4_0}[_batch|_vnorm] (kernels.metal:1197-1436;

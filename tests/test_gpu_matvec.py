@@ -170,3 +170,41 @@ def test_matvec_invalid_input(rt):
         with pytest.raises(OperatorError) as e:
             bad()
         assert e.value.kind == "InvalidInput"
+
+
+def _gelu64(x):
+    a = 0.7978845608 * (x + 0.044715 * x ** 3)
+    return 0.5 * x * (1.0 + np.tanh(a))
+
+
+@pytest.mark.parametrize("n,m,layers", [(1536, 256, 35), (2048, 64, 3), (32, 5, 2), (4096, 300, 1)])
+def test_ple_gate_gelu(rt, ora, n, m, layers):
+    """gemma4_ple_gate_gelu_f32 (kernels.metal:803-881): gelu(W . state) * ple[offset + o]
+    for each layer's slice.  The projection error (<= TOL * magnitude, as above) passes
+    through GELU (|gelu'| < 1.13) and the f32 GELU adds a few ulp of |x|."""
+    r = np.random.default_rng(500 + n + m)
+    x = (0.3 * r.standard_normal(n)).astype(f32)
+    W = mc.random_q4_0(r, m, n)
+    ple = r.standard_normal(layers * m).astype(f32)
+    dx, dW, dp, out = rt.upload(x), rt.upload(W), rt.upload(ple), rt.empty(m)
+    g64, mag = ora.matvec_q4_0_rms_f64(x, W, None, n, m, EPS)
+    for layer in range(layers):
+        say(f"ple gate n={n} out={m} layer={layer}")
+        rt.ple_gate_gelu(dx, dW, dp, layer * m, out, n, m)
+        rt.sync()
+        got = out.download(m).astype(np.float64)
+        p = ple[layer * m:(layer + 1) * m].astype(np.float64)
+        exact = _gelu64(g64) * p
+        bound = (1.2 * TOL * mag + 8 * 2.0 ** -24 * (np.abs(g64) + 1.0)) * np.abs(p) + 2.0 ** -23 * np.abs(exact)
+        assert np.all(np.abs(got - exact) <= bound), float(np.max(np.abs(got - exact) / bound))
+
+
+def test_ple_gate_invalid_input(rt):
+    say("ple gate invalid input")
+    x, W, p, out = rt.empty(1536), rt.empty(4096), rt.empty(256), rt.empty(256)
+    for bad in (lambda: rt.ple_gate_gelu(x, W, None, 0, out, 1536, 256),
+                lambda: rt.ple_gate_gelu(x, W, p, 0, out, 1000, 256),
+                lambda: rt.ple_gate_gelu(x, W, p, 0, out, 1536, 0)):
+        with pytest.raises(OperatorError) as e:
+            bad()
+        assert e.value.kind == "InvalidInput"
