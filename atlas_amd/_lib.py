@@ -108,6 +108,9 @@ SIGNATURES = {
     "atlas_hip_kv_append_f32": [CTX, P, P, P, U32, U32, P, U32, c_int, F],
     "atlas_hip_kv_append_q8_0": [CTX, P, P, P, U32, U32, P, U32, c_int, F],
     "atlas_hip_kv_append_q4_0": [CTX, P, P, P, U32, U32, P, U32, c_int, F],
+    "atlas_hip_softcap_f32": [CTX, P, P, U64, F],
+    "atlas_hip_argmax_f32": [CTX, P, P, U32, U32],
+    "atlas_hip_softcap_argmax_f32": [CTX, P, P, P, U32, U32, F],
     "atlas_ops_embedding": [CTX, P, SZ, SZ, SZ, P, SZ, P, SZ, TIMING],
     "atlas_ops_embedding_q6_k": [CTX, P, SZ, SZ, SZ, P, SZ, P, SZ, TIMING],
     "atlas_ops_add": [CTX, P, SZ, P, SZ, P, SZ, TIMING],

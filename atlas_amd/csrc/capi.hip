@@ -23,6 +23,9 @@ struct atlas_hip_ctx {
     hipStream_t stream = nullptr;
     int reduction = ATLAS_REDUCTION_SEQUENTIAL;
     bool capturing = false;
+    // argmax workspace (per-workgroup partial keys of the rows being
+    // reduced): allocated once here, never inside an op
+    void* argmax_ws = nullptr;
     std::string last_error;
     atlas_hip_telemetry tel{};
 };
@@ -114,6 +117,13 @@ int atlas_hip_init(int device, atlas_hip_ctx** out) {
         return ATLAS_ERR_COMMAND_FAILED;
     }
     ctx->stream = ctx->own_stream;
+    e = hipMalloc(&ctx->argmax_ws, atlas::argmax_workspace_bytes());
+    if (e != hipSuccess) {
+        if (ctx->argmax_ws) (void)hipFree(ctx->argmax_ws);
+        (void)hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return e == hipErrorOutOfMemory ? ATLAS_ERR_OUT_OF_MEMORY : ATLAS_ERR_COMMAND_FAILED;
+    }
     *out = ctx;
     return ATLAS_OK;
 }
@@ -123,6 +133,10 @@ void atlas_hip_destroy(atlas_hip_ctx* ctx) {
     if (enter(ctx) == ATLAS_OK && ctx->own_stream) {
         (void)hipStreamSynchronize(ctx->own_stream);
         (void)hipStreamDestroy(ctx->own_stream);
+    }
+    if (ctx->argmax_ws && enter(ctx) == ATLAS_OK) {
+        (void)hipDeviceSynchronize();  // a caller stream may still use it
+        (void)hipFree(ctx->argmax_ws);
     }
     delete ctx;
 }
@@ -739,6 +753,48 @@ int atlas_hip_kv_append_q4_0(atlas_hip_ctx* ctx, const float* key, const float* 
                              int vnorm, float epsilon) {
     return kv_append(ctx, atlas::kKvQ4_0, key, value, cache, kv_width, capacity, positions, tokens, vnorm, epsilon,
                      "kv_append_q4_0");
+}
+
+// ---------------------------------------------------------------------------
+// logits: soft cap and argmax
+// ---------------------------------------------------------------------------
+
+static bool finite_cap(float cap) { return std::isfinite(cap) && cap > 0.0f; }
+
+int atlas_hip_softcap_f32(atlas_hip_ctx* ctx, const float* input, float* output, uint64_t count, float cap) {
+    int rc = enter(ctx);
+    if (rc) return rc;
+    if (!input || !output) return invalid(ctx, "soft cap buffer is null");
+    if (count == 0) return invalid(ctx, "soft cap needs at least one value");
+    // gemma4_softcap_logits: "Gemma 4 logit soft cap must be positive"
+    if (!finite_cap(cap)) return invalid(ctx, "logit soft cap must be finite and positive");
+    if ((reinterpret_cast<uintptr_t>(input) | reinterpret_cast<uintptr_t>(output)) & 3)
+        return invalid(ctx, "logits must be 4-byte aligned");
+    return launched(ctx, atlas::launch_softcap_f32(ctx->stream, input, output, count, cap), "softcap_f32");
+}
+
+static int logits_rows(atlas_hip_ctx* ctx, const float* logits, float* capped, uint32_t* selected, uint32_t rows,
+                       uint32_t count, float cap, const char* op) {
+    int rc = enter(ctx);
+    if (rc) return rc;
+    if (!logits || !selected) return invalid(ctx, "argmax buffer is null");
+    // argmax_for_test: "argmax requires at least one value"
+    if (rows == 0 || count == 0) return invalid(ctx, "argmax requires at least one value per row");
+    if ((reinterpret_cast<uintptr_t>(logits) | reinterpret_cast<uintptr_t>(capped) |
+         reinterpret_cast<uintptr_t>(selected)) & 3)
+        return invalid(ctx, "logits and selected must be 4-byte aligned");
+    return launched(ctx, atlas::launch_logits_f32(ctx->stream, logits, capped, selected, rows, count, cap, ctx->argmax_ws),
+                    op);
+}
+
+int atlas_hip_argmax_f32(atlas_hip_ctx* ctx, const float* values, uint32_t* selected, uint32_t rows, uint32_t count) {
+    return logits_rows(ctx, values, nullptr, selected, rows, count, 0.0f, "argmax_f32");
+}
+
+int atlas_hip_softcap_argmax_f32(atlas_hip_ctx* ctx, const float* logits, float* capped, uint32_t* selected,
+                                 uint32_t rows, uint32_t count, float cap) {
+    if (ctx && !finite_cap(cap)) return invalid(ctx, "logit soft cap must be finite and positive");
+    return logits_rows(ctx, logits, capped, selected, rows, count, cap, "softcap_argmax_f32");
 }
 
 int atlas_hip_ple_q4_0(atlas_hip_ctx* ctx, const uint8_t* table, const uint32_t* ids, const float* projection,

@@ -126,4 +126,19 @@ struct KvAppendArgs {
 };
 hipError_t launch_kv_append(hipStream_t stream, int format, bool vnorm, const KvAppendArgs& a);
 
+// Logit soft cap and argmax (logits_kernels.hip).  The argmax of a row split
+// over several workgroups goes through a workspace owned by the context:
+// one 64-bit slot per workgroup (at most kArgmaxSlotsPerRow per row), written
+// by the streaming launch and reduced by a second launch; every slot read is
+// written by the same call first, so the workspace needs no clearing.
+constexpr uint32_t kArgmaxSlotsPerRow = 256;
+constexpr uint32_t kArgmaxSlots = 65536;  // 512 KiB
+size_t argmax_workspace_bytes();
+// cap > 0: capped = cap * tanh(logits / cap) (capped may alias logits or be
+// null when only the argmax is wanted); selected != null: selected[r] =
+// argmax of row r of the (capped) logits.  rows x count values, count >= 1.
+hipError_t launch_logits_f32(hipStream_t stream, const float* logits, float* capped, uint32_t* selected,
+                             uint32_t rows, uint32_t count, float cap, void* workspace);
+hipError_t launch_softcap_f32(hipStream_t stream, const float* in, float* out, uint64_t n, float cap);
+
 }  // namespace atlas

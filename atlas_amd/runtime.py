@@ -292,6 +292,17 @@ class HipRuntime:
         self._check(fn(self.ctx, _ptr(key), _ptr(value), _ptr(cache), kv_width, capacity, _ptr(positions), tokens,
                        1 if vnorm else 0, eps))
 
+    # Decode tail: softcap_f32 / argmax_f32 (kernels.metal:931-934, 2033-2066)
+    def softcap(self, x, y, n, cap):
+        self._check(self.lib.atlas_hip_softcap_f32(self.ctx, _ptr(x), _ptr(y), n, cap))
+
+    def argmax(self, values, selected, rows, count):
+        self._check(self.lib.atlas_hip_argmax_f32(self.ctx, _ptr(values), _ptr(selected), rows, count))
+
+    def softcap_argmax(self, logits, capped, selected, rows, count, cap):
+        self._check(self.lib.atlas_hip_softcap_argmax_f32(self.ctx, _ptr(logits), _ptr(capped), _ptr(selected), rows,
+                                                          count, cap))
+
     def matmul_q4_0_gate_up_rms(self, x, gw, uw, g_out, u_out, input_width, output_width, rms_weight, eps):
         self._check(self.lib.atlas_hip_matmul_q4_0_gate_up_rms_f32(self.ctx, _ptr(x), _ptr(gw), _ptr(uw), _ptr(g_out),
                                                                    _ptr(u_out), input_width, output_width,

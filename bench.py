@@ -26,6 +26,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--reduction sequenti
        python bench.py --copy-mib 256               (a D2D copy of known size: the PMC
                                                       calibration kernel)
        python bench.py --decode                     (configs[4] batched decode, separate line)
+       python bench.py --config c1|c2|gemv|kv|logits (other op configurations, per-op lines)
 """
 import argparse
 import json
@@ -130,7 +131,8 @@ class ConfigOps(Ops):
     c1 = BASELINE configs[0] (SmolLM2-135M-shaped FP32 ops, T=128),
     c2 = BASELINE configs[1] (SmolLM2-1.7B-shaped FP16 storage, T=2048),
     gemv = the RMS-folded Q4_0 decode projections of one Gemma-4-E2B-like token,
-    kv = the KV append with the fused V RMSNorm (prefill batch and one decode token)."""
+    kv = the KV append with the fused V RMSNorm (prefill batch and one decode token),
+    logits = the soft cap + greedy argmax decode tail (256 sequences and one token)."""
 
     def __init__(self, wl, rope_tables, cfg):
         r = wl.rng(2025)
@@ -198,6 +200,21 @@ class ConfigOps(Ops):
             self.table["kv_append_q4_0_vnorm_decode"] = (
                 ["k", "v", "pos1"], {"c1": 2 * cap * rows["q4_0"] // 4}, 2 * W * 4 + 4 + 2 * rows["q4_0"],
                 lambda rt, s: rt.kv_append("q4_0", s["k"], s["v"], s["c1"], W, cap, s["pos1"], 1, True, L.eps))
+        elif cfg == "logits":
+            # the decode tail, soft cap (30) + greedy argmax
+            # over the 262144-entry vocabulary: the C5 batch of 256 sequences
+            # (in place, as the reference caps its logits buffer) and one token
+            V, cap = wl.QuantGatherShape().vocab, 30.0
+            self.tokens = 256
+            self.host = {"l256": wl.normal(r, 256 * V, 0.0, 10.0), "l1": wl.normal(r, V, 0.0, 10.0)}
+            self.table = {
+                "softcap_argmax_B256": (["l256"], {"s256": 256}, 2 * 256 * V * 4 + 256 * 4,
+                                        lambda rt, s: rt.softcap_argmax(s["l256"], s["l256"], s["s256"], 256, V, cap)),
+                "argmax_B256": (["l256"], {"a256": 256}, 256 * V * 4 + 256 * 4,
+                                lambda rt, s: rt.argmax(s["l256"], s["a256"], 256, V)),
+                "softcap_argmax_B1": (["l1"], {"s1": 1}, 2 * V * 4 + 4,
+                                      lambda rt, s: rt.softcap_argmax(s["l1"], s["l1"], s["s1"], 1, V, cap)),
+            }
         else:
             S = wl.SmolShape()
             T, H, QH, KH, D, F, V = S.tokens, S.hidden, S.q_heads, S.kv_heads, S.head_dim, S.ffn, S.vocab
@@ -345,10 +362,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma-separated op subset: per-op timing only (profiling)")
     ap.add_argument("--copy-mib", type=int, default=0, help="also time a device-to-device copy of this size")
-    ap.add_argument("--config", choices=["c3c4", "c1", "c2", "gemv", "kv"], default="c3c4",
+    ap.add_argument("--config", choices=["c3c4", "c1", "c2", "gemv", "kv", "logits"], default="c3c4",
                     help="c1 / c2: per-op lines for BASELINE configs[0] / configs[1]; gemv: the RMS-folded "
-                         "Q4_0 decode projections of one token; kv: the KV append with the fused V norm "
-                         "-- instead of the headline")
+                         "Q4_0 decode projections of one token; kv: the KV append with the fused V norm; "
+                         "logits: the soft cap + argmax decode tail -- instead of the headline")
     ap.add_argument("--decode", action="store_true",
                     help="BASELINE configs[4] batched decode (per-layer latency, eager and HIP graph) instead")
     args = ap.parse_args()
@@ -374,7 +391,7 @@ def main():
         for name, (_, _, nbytes, launch) in cops.table.items():
             # the weight-streaming projections need >= 1 GiB of distinct weights
             # to keep the 256 MB MALL out of the measurement
-            cap = 1024 if args.config in ("gemv", "kv") else 64
+            cap = 1024 if args.config in ("gemv", "kv", "logits") else 64
             nsets = min(cap, max(4, math.ceil(ROTATION_BYTES / cops.set_bytes(name))))
             log(f"timing {args.config} {name} ({nsets} rotating sets)")
             sets = cops.build_sets(rt, [name], nsets)

@@ -336,6 +336,33 @@ int atlas_hip_kv_append_q4_0(atlas_hip_ctx *ctx, const float *key, const float *
                              uint32_t kv_width, uint32_t capacity, const uint32_t *positions,
                              uint32_t tokens, int vnorm, float epsilon);
 
+/* ---- logits: soft cap and greedy argmax (decode tail) -------------------- */
+
+/* softcap_f32 (kernels.metal:931-934; callers gemma4_executor.rs:3673-3676,
+ * 4678-4682; CPU form gemma4_softcap_logits,
+ * crates/atlas-model/src/lib.rs:223-232): output = cap * tanh(input / cap)
+ * over `count` values; output may alias input (the reference caps in
+ * place).  cap must be finite and positive, as gemma4_softcap_logits
+ * ensures.  The tanh is this library's (within 1.4 ulp of float64); the
+ * reference's Metal/libm tanh bits are not reproducible off Apple, so parity
+ * with the reference is the operator tolerance, bit-exact with the oracle. */
+int atlas_hip_softcap_f32(atlas_hip_ctx *ctx, const float *input, float *output, uint64_t count, float cap);
+/* argmax_f32 (kernels.metal:2033-2066; callers gemma4_executor.rs:3678-3683,
+ * 4683-4688, executor.rs:1381 via dispatch_decode_argmax :1515): for each of
+ * `rows` rows of `count` values, selected[r] = the largest index holding the
+ * row's maximum (the reference's tie rule: the later token id wins); NaN is
+ * never selected and +0 equals -0, as under the kernel's comparisons; a row
+ * of NaN selects 0.  count >= 1 (argmax_for_test, lib.rs:1623-1628). */
+int atlas_hip_argmax_f32(atlas_hip_ctx *ctx, const float *values, uint32_t *selected, uint32_t rows,
+                         uint32_t count);
+/* softcap_f32 followed by argmax_f32, the decode tail of
+ * encode_current_token (gemma4_executor.rs:4678-4688), in one pass:
+ * capped = cap * tanh(logits / cap) (may alias logits; NULL skips the
+ * store), selected[r] = argmax of capped row r.  Same results as the two
+ * entry points above in sequence. */
+int atlas_hip_softcap_argmax_f32(atlas_hip_ctx *ctx, const float *logits, float *capped, uint32_t *selected,
+                                 uint32_t rows, uint32_t count, float cap);
+
 /* ---- host-slice operator API (atlas_ops::NeuralOps) --------------------- */
 
 /* NeuralOps::embedding -> MetalRuntime::embedding_lookup (lib.rs:1393-1433). */

@@ -800,3 +800,76 @@ void oracle_kv_append(int format, const float *key, const float *value, uint8_t 
     }
 }
 
+
+/* ======================================================================== */
+/* logits: soft cap and argmax                                              */
+/* ======================================================================== */
+
+/* Coefficients of the Maclaurin series of tanh,
+ * tanh(a) = sum_n 2^{2n} (2^{2n} - 1) B_{2n} a^{2n-1} / (2n)!  (B = Bernoulli
+ * numbers): -1/3, 2/15, -17/315, 62/2835, -1382/155925, 21844/6081075,
+ * -929569/638512875, 6404582/10854718875, -443861162/1856156927625, each
+ * rounded to binary32. */
+static const float kTanhSeries[9] = {
+    -0x1.555556p-2f, 0x1.111112p-3f, -0x1.ba1ba2p-5f, 0x1.664f48p-6f, -0x1.226e36p-7f,
+    0x1.d6d3d0p-9f,  -0x1.7da364p-10f, 0x1.355824p-11f, -0x1.f57d78p-13f,
+};
+
+/* tanh for the logit soft cap.  The reference evaluates Metal's built-in
+ * tanh on the GPU (softcap_f32, crates/atlas-metal/src/kernels.metal:931-934)
+ * and Rust's f32::tanh on the CPU (gemma4_softcap_logits,
+ * crates/atlas-model/src/lib.rs:223-232); neither is reproducible here, so
+ * this is a restated method pinned against float64: for |x| < 0.625 the
+ * series above through a^19 (truncation < 2^-28 relative), evaluated as
+ * a + (a*z)*P(z), z = a*a, in Horner form with fmaf; above, the identity
+ * 1 - 2/(e^{2a} + 1) with oracle_expf, saturating to 1 once e^{2a}
+ * overflows.  The sign is copied from x; NaN propagates.  Within 1.4 ulp of
+ * float64 tanh over every binary32 input (tests/test_oracle_pins.py). */
+float oracle_tanh_precise(float x) {
+    const float a = fabsf(x);
+    if (a < 0.625f) {
+        const float z = a * a;
+        float p = kTanhSeries[8];
+        for (int i = 7; i >= 0; --i) p = fmaf(p, z, kTanhSeries[i]);
+        return copysignf(fmaf(a * z, p, a), x);
+    }
+    const float e = oracle_expf(2.0f * a);
+    return copysignf(1.0f - 2.0f / (e + 1.0f), x);
+}
+
+/* softcap_f32 (kernels.metal:931-934) = gemma4_softcap_logits
+ * (crates/atlas-model/src/lib.rs:223-232): v = cap * tanh(v / cap), applied
+ * to `n` values. */
+void oracle_softcap_f32(const float *input, float *output, size_t n, float cap) {
+    for (size_t i = 0; i < n; ++i) output[i] = cap * oracle_tanh_precise(input[i] / cap);
+}
+
+/* argmax_f32 (kernels.metal:2033-2066): every lane scans its stride with
+ * `value >= best` from (-inf, 0) and the tree keeps the larger value, or the
+ * larger index on equal values.  The result is therefore the largest index
+ * holding the maximum of the non-NaN values (NaN compares false and is never
+ * taken; +0 and -0 compare equal), and 0 when every value is NaN.  A single
+ * left-to-right scan with the same `>=` gives the same index. */
+uint32_t oracle_argmax_f32(const float *values, size_t count) {
+    float best = -INFINITY;
+    uint32_t id = 0;
+    for (size_t i = 0; i < count; ++i) {
+        if (values[i] >= best) {
+            best = values[i];
+            id = (uint32_t)i;
+        }
+    }
+    return id;
+}
+
+/* The decode tail of the Gemma executor for `rows` sequences
+ * (gemma4_executor.rs:4678-4688): softcap_f32 over each row of `count`
+ * logits in place, then argmax_f32 of the capped row.  cap <= 0 skips the
+ * soft cap (argmax only). */
+void oracle_softcap_argmax_rows(float *logits, uint32_t *selected, size_t rows, size_t count, float cap) {
+    for (size_t r = 0; r < rows; ++r) {
+        float *row = logits + r * count;
+        if (cap > 0.0f) oracle_softcap_f32(row, row, count, cap);
+        selected[r] = oracle_argmax_f32(row, count);
+    }
+}

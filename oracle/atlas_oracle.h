@@ -28,6 +28,12 @@
  *   - PLE combine:     reference KAT (gemma4_primitives.rs:3-10).
  *   - fused epilogues: equal to the composition of the unfused oracle steps
  *                      (the reference's dispatch_fusion_parity.rs contract).
+ *   - tanh_precise:    float64 tanh (< 1.4 ulp over a dense binary32 sweep)
+ *                      and glibc tanhf (<= 2 ulp); soft-cap KAT
+ *                      (gemma4_primitives.rs:13-19).
+ *   - argmax:          the reference's large-vocabulary tie KAT
+ *                      (crates/atlas-metal/src/lib.rs:2217-2230), numpy argmax
+ *                      of the reversed row, brute-force tie/NaN/-0 cases.
  */
 #ifndef ATLAS_ORACLE_H
 #define ATLAS_ORACLE_H
@@ -157,6 +163,14 @@ void oracle_encode_q8_0_block(const float *v, uint8_t *out34);
 void oracle_encode_q4_0_block(const float *v, uint8_t *out18);
 void oracle_kv_append(int format, const float *key, const float *value, uint8_t *cache, size_t kv_width,
                       size_t capacity, const uint32_t *positions, size_t tokens, int vnorm, float epsilon);
+
+/* Logits: soft cap (softcap_f32, kernels.metal:931-934; CPU
+ * gemma4_softcap_logits, crates/atlas-model/src/lib.rs:223-232) and argmax
+ * (argmax_f32, kernels.metal:2033-2066). */
+float oracle_tanh_precise(float x);
+void oracle_softcap_f32(const float *input, float *output, size_t n, float cap);
+uint32_t oracle_argmax_f32(const float *values, size_t count);
+void oracle_softcap_argmax_rows(float *logits, uint32_t *selected, size_t rows, size_t count, float cap);
 
 #ifdef __cplusplus
 }

@@ -66,6 +66,10 @@ _SIGS = {
     "oracle_add_f32": ([P, P, P, SZ], None),
     "oracle_multiply_f32": ([P, P, P, SZ], None),
     "oracle_scale_f32": ([P, F, P, SZ], None),
+    "oracle_tanh_precise": ([F], c_float),
+    "oracle_softcap_f32": ([P, P, SZ, F], None),
+    "oracle_argmax_f32": ([P, SZ], ctypes.c_uint32),
+    "oracle_softcap_argmax_rows": ([P, P, SZ, SZ, F], None),
 }
 
 _lib = None
@@ -386,3 +390,29 @@ def encode_q4_0_block(values):
     lib().oracle_encode_q4_0_block(_p(v), _p(out))
     return out
 
+
+
+def tanh_precise(x):
+    """tanh of the logit soft cap, elementwise over a float32 array."""
+    x = _c(x, f32)
+    return np.array([lib().oracle_tanh_precise(float(v)) for v in x.ravel()], f32).reshape(x.shape)
+
+
+def softcap(x, cap):
+    x = _c(x, f32)
+    out = np.empty_like(x)
+    lib().oracle_softcap_f32(_p(x), _p(out), x.size, cap)
+    return out
+
+
+def argmax(values):
+    v = _c(values, f32)
+    return int(lib().oracle_argmax_f32(_p(v), v.size))
+
+
+def softcap_argmax_rows(logits, rows, count, cap):
+    """Returns (capped logits, selected ids); cap <= 0 skips the soft cap."""
+    x = _c(logits, f32).copy()
+    sel = np.empty(rows, u32)
+    lib().oracle_softcap_argmax_rows(_p(x), _p(sel), rows, count, cap)
+    return x, sel

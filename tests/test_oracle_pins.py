@@ -555,3 +555,98 @@ def test_kv_append_layout_and_vnorm(ora):
     untouched = [1, 3, 5]
     raw = cache.view(f32).reshape(2, cap, w)
     assert np.array_equal(out[:, untouched].view(np.uint32), raw[:, untouched].view(np.uint32))
+
+
+# ------------------------------------------------------------ logits tail
+
+def test_tanh_precise_against_float64(ora):
+    """The soft cap's tanh: dense sweep of binary32 inputs against float64
+    (softcap with cap 1 is tanh itself: x/1 and 1*t are exact)."""
+    bits = np.arange(0, 0x7F800000, 61, dtype=np.uint32)
+    x = bits.view(f32)
+    got = ora.softcap(x, 1.0)
+    err = ulp_err(got, np.tanh(x.astype(np.float64)))
+    assert float(err.max()) < 1.4, f"tanh worst {float(err.max()):.3f} ulp"
+    # odd symmetry, signed zero, saturation, NaN, subnormals pass through
+    assert np.array_equal(ora.softcap(-x[:200000], 1.0).view(np.uint32),
+                          (-got[:200000]).view(np.uint32))
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-40, 10.0, 1e30], f32)
+    s = ora.softcap(special, 1.0)
+    assert s[0] == 0 and not np.signbit(s[0]) and s[1] == 0 and np.signbit(s[1])
+    assert s[2] == 1 and s[3] == -1 and np.isnan(s[4])
+    assert s[5] == special[5] and s[6] == special[6] and s[7] == 1 and s[8] == 1
+
+
+def test_softcap_kat_and_cpu_form(ora):
+    k = KATS["softcap"]
+    v = ora.softcap(np.array(k["logits"], f32), k["cap"])
+    assert np.all(np.abs(v) <= k["cap"])
+    assert np.all(np.diff(v) > 0)
+    assert abs(float(v[2])) < np.finfo(f32).eps
+    # the reference CPU form cap * (x / cap).tanh() in binary32 (numpy's tanh
+    # standing in for Rust's libm): within the operator tolerance of 4 ulp
+    r = np.random.default_rng(31)
+    x = np.concatenate([r.normal(0, 10, 200000), r.normal(0, 100, 50000), r.uniform(-1e4, 1e4, 50000)]).astype(f32)
+    cap = f32(30.0)
+    got = ora.softcap(x, cap)
+    cpu_form = (cap * np.tanh(x / cap)).astype(f32)
+    assert float(ulp_err(got, cpu_form).max()) <= 4.0
+    exact = 30.0 * np.tanh(x.astype(np.float64) / 30.0)
+    assert float(ulp_err(got, exact).max()) <= 2.5
+
+
+def _reference_argmax_kernel(values):
+    """The reference kernel's structure, step by step (kernels.metal:2033-2066):
+    256 lanes scan their stride with `>=` from (-inf, 0), then the tree."""
+    vals = [float(v) for v in values]
+    best = [(-np.inf, 0)] * 256
+    for lane in range(256):
+        bv, bi = -np.inf, 0
+        for i in range(lane, len(vals), 256):
+            if vals[i] >= bv:
+                bv, bi = vals[i], i
+        best[lane] = (bv, bi)
+    stride = 128
+    while stride:
+        for lane in range(stride):
+            ov, oi = best[lane + stride]
+            cv, ci = best[lane]
+            if ov > cv or (ov == cv and oi >= ci):
+                best[lane] = (ov, oi)
+        stride >>= 1
+    return best[0][1]
+
+
+def test_argmax_kat_and_kernel_structure(ora):
+    k = KATS["argmax"]
+    v = np.full(k["count"], k["fill"], f32)
+    for i, val in k["set"]:
+        v[i] = val
+    assert ora.argmax(v) == k["expected"]
+    r = np.random.default_rng(5)
+    pool = np.array([-1.0, 0.0, -0.0, 1.0, 2.0, -np.inf, np.inf, np.nan], f32)
+    for trial in range(300):
+        n = int(r.integers(1, 700))
+        vals = pool[r.integers(0, len(pool) - (0 if trial % 3 else 2), n)]
+        assert ora.argmax(vals) == _reference_argmax_kernel(vals), vals
+    for vals in (np.full(5, np.nan, f32), np.full(300, -np.inf, f32), np.array([-0.0, 0.0, -0.0], f32)):
+        assert ora.argmax(vals) == _reference_argmax_kernel(vals)
+    # NaN-free rows without signed-zero ties: also the CPU executor's argmax
+    # (max_by over total_cmp keeps the last maximum, atlas-model/src/lib.rs:1469-1476)
+    for _ in range(50):
+        vals = r.integers(-20, 20, int(r.integers(1, 5000))).astype(f32)
+        vals[vals == 0] = 1.0
+        assert ora.argmax(vals) == len(vals) - 1 - int(np.argmax(vals[::-1]))
+
+
+def test_softcap_argmax_rows_is_the_composition(ora):
+    r = np.random.default_rng(9)
+    rows, count = 5, 3001
+    x = r.normal(0, 20, rows * count).astype(f32)
+    capped, sel = ora.softcap_argmax_rows(x, rows, count, 30.0)
+    assert np.array_equal(capped.view(np.uint32), ora.softcap(x, 30.0).view(np.uint32))
+    for i in range(rows):
+        assert sel[i] == ora.argmax(capped[i * count:(i + 1) * count])
+    plain, sel0 = ora.softcap_argmax_rows(x, rows, count, 0.0)
+    assert np.array_equal(plain.view(np.uint32), x.view(np.uint32))
+    assert all(sel0[i] == ora.argmax(x[i * count:(i + 1) * count]) for i in range(rows))
