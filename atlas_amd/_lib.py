@@ -41,6 +41,13 @@ class Telemetry(ctypes.Structure):
     ]
 
 
+class GgufTensor(ctypes.Structure):
+    """atlas_gguf_tensor (include/atlas_gguf.h): GgufTensor, crates/atlas-core/src/gguf.rs:80-87."""
+
+    _fields_ = [("name", c_void_p), ("name_len", c_uint64), ("n_dims", c_uint32), ("dims", c_uint64 * 4), ("type", c_uint32),
+                ("offset", c_uint64), ("bytes", c_uint64)]
+
+
 P = c_void_p  # device or host pointer
 CTX = c_void_p
 F = c_float
@@ -111,6 +118,23 @@ SIGNATURES = {
     "atlas_hip_softcap_f32": [CTX, P, P, U64, F],
     "atlas_hip_argmax_f32": [CTX, P, P, U32, U32],
     "atlas_hip_softcap_argmax_f32": [CTX, P, P, P, U32, U32, F],
+    "atlas_gguf_open": [c_char_p, POINTER(c_void_p), c_char_p, SZ],
+    "atlas_gguf_from_bytes": [P, SZ, POINTER(c_void_p), c_char_p, SZ],
+    "atlas_gguf_close": [P],
+    "atlas_gguf_tensor_count": [P],
+    "atlas_gguf_tensor_info": [P, U64, POINTER(GgufTensor)],
+    "atlas_gguf_find_tensor": [P, c_char_p],
+    "atlas_gguf_tensor_data": [P, U64, POINTER(c_void_p), POINTER(c_uint64)],
+    "atlas_gguf_upload_tensor": [CTX, P, U64, P],
+    "atlas_gguf_metadata_count": [P],
+    "atlas_gguf_metadata_entry": [P, U64, POINTER(c_void_p), POINTER(c_uint64), POINTER(c_void_p),
+                                  POINTER(c_uint64)],
+    "atlas_gguf_metadata_get": [P, c_char_p],
+    "atlas_gguf_metadata_array_count": [P],
+    "atlas_gguf_metadata_array_entry": [P, U64, POINTER(c_void_p), POINTER(c_uint64), POINTER(c_uint32),
+                                        POINTER(c_uint64), POINTER(c_void_p)],
+    "atlas_gguf_metadata_array_string": [P, U64, U64, POINTER(c_void_p), POINTER(c_uint64)],
+    "atlas_gguf_find_metadata_array": [P, c_char_p],
     "atlas_ops_embedding": [CTX, P, SZ, SZ, SZ, P, SZ, P, SZ, TIMING],
     "atlas_ops_embedding_q6_k": [CTX, P, SZ, SZ, SZ, P, SZ, P, SZ, TIMING],
     "atlas_ops_add": [CTX, P, SZ, P, SZ, P, SZ, TIMING],
@@ -123,6 +147,13 @@ SIGNATURES = {
 }
 
 _RESTYPES = {
+    "atlas_gguf_close": None,
+    "atlas_gguf_tensor_count": c_uint64,
+    "atlas_gguf_find_tensor": ctypes.c_int64,
+    "atlas_gguf_metadata_count": c_uint64,
+    "atlas_gguf_metadata_get": c_char_p,
+    "atlas_gguf_metadata_array_count": c_uint64,
+    "atlas_gguf_find_metadata_array": ctypes.c_int64,
     "atlas_hip_destroy": None,
     "atlas_hip_get_stream": c_void_p,
     "atlas_hip_last_error": c_char_p,

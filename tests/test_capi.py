@@ -1,5 +1,5 @@
 """CPU checks of the C ABI: the library loads, exports exactly what
-include/atlas_hip_ops.h declares, behaves like MetalError::NoDevice when no
+include/atlas_hip_ops.h and include/atlas_gguf.h declare, behaves like MetalError::NoDevice when no
 GPU is present, and its host-only helpers (RoPE tables) agree bit-for-bit
 with the oracle.  No kernel is launched here."""
 import ctypes
@@ -14,13 +14,15 @@ import atlas_amd
 from atlas_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "atlas_hip_ops.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("atlas_hip_ops.h", "atlas_gguf.h")]
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(atlas_(?:hip|ops|rope)_\w+)\s*\(", text)))
+    names = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(header).read(), flags=re.S)
+        names |= set(re.findall(r"\b(atlas_(?:hip|ops|rope|gguf)_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def exported_symbols():
