@@ -130,7 +130,7 @@ class ConfigOps(Ops):
     """Per-op timing at the other op configurations (separate lines, not the headline):
     c1 = BASELINE configs[0] (SmolLM2-135M-shaped FP32 ops, T=128),
     c2 = BASELINE configs[1] (SmolLM2-1.7B-shaped FP16 storage, T=2048),
-    gemv = the RMS-folded Q4_0 decode projections of one Gemma-4-E2B-like token,
+    gemv = the RMS-folded Q4_0 decode projections and the PLE input gate of one Gemma-4-E2B-like token,
     kv = the KV append with the fused V RMSNorm (prefill batch and one decode token),
     logits = the soft cap + greedy argmax decode tail (256 sequences and one token)."""
 
@@ -167,9 +167,11 @@ class ConfigOps(Ops):
             H, QN, KVN, F = L.hidden, L.q_heads * L.head_dim, L.head_dim, L.ffn
             rb = wl.q_row_bytes(H, False)
             self.tokens = 1
+            PW, PL = wl.QuantGatherShape().ple_width, wl.QuantGatherShape().ple_layers
             self.host = {"x": wl.normal(r, H), "w": wl.normal(r, H, 1.0, 0.1), "qw": wl.q4_0_table(r, QN, H),
                          "kw": wl.q4_0_table(r, KVN, H), "vw": wl.q4_0_table(r, KVN, H),
-                         "gw": wl.q4_0_table(r, F, H), "uw": wl.q4_0_table(r, F, H)}
+                         "gw": wl.q4_0_table(r, F, H), "uw": wl.q4_0_table(r, F, H),
+                         "pgw": wl.q4_0_table(r, PW, H), "ple": wl.normal(r, PL * PW)}
             eps = L.eps
             self.table = {
                 "qkv_rms": (["x", "w", "qw", "kw", "vw"], {"qo": QN, "ko": KVN, "vo": KVN},
@@ -179,6 +181,10 @@ class ConfigOps(Ops):
                 "gate_up_rms": (["x", "w", "gw", "uw"], {"go": F, "uo": F}, 2 * F * rb + 2 * H * 4 + 2 * F * 4,
                                 lambda rt, s: rt.matmul_q4_0_gate_up_rms(s["x"], s["gw"], s["uw"], s["go"], s["uo"],
                                                                          H, F, s["w"], eps)),
+                # the PLE input gate of one layer (256 rows, layer 17's PLE slice)
+                "ple_gate_gelu": (["x", "pgw", "ple"], {"pgo": PW}, PW * rb + H * 4 + PW * 4 + PW * 4,
+                                  lambda rt, s: rt.ple_gate_gelu(s["x"], s["pgw"], s["ple"], 17 * PW, s["pgo"], H,
+                                                                 PW)),
             }
         elif cfg == "kv":
             # KV append with the fused V RMSNorm at the
