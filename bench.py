@@ -258,6 +258,32 @@ def time_launches(rt, launch, sets, iters):
     return rt.elapsed_ms(a, b) / iters
 
 
+def copy_reference_us(rt, nbytes, iters):
+    """Size-matched memory-system reference for an op that moves `nbytes`: the
+    runtime's device-to-device copy of nbytes/2 (nbytes/2 read + nbytes/2
+    written), timed like the ops (HIP events around back-to-back launches,
+    rotating over >= 1 GiB of distinct buffers)."""
+    half = max(16, (nbytes // 2) // 16 * 16)
+    npairs = max(4, math.ceil(ROTATION_BYTES / (2 * half)))
+    pairs = [(rt.alloc(half), rt.alloc(half)) for _ in range(npairs)]
+    for src, _ in pairs:
+        rt.memset(src, 0, half)
+    for i in range(3):
+        rt.copy(pairs[i % npairs][1], pairs[i % npairs][0], half)
+    rt.sync()
+    a, b = rt.event(), rt.event()
+    rt.record(a)
+    for i in range(iters):
+        rt.copy(pairs[i % npairs][1], pairs[i % npairs][0], half)
+    rt.record(b)
+    rt.sync()
+    us = rt.elapsed_ms(a, b) / iters * 1e3
+    for src, dst in pairs:
+        rt.free(src)
+        rt.free(dst)
+    return us
+
+
 def cpu_baseline(wl, budget_s=10.0):
     """Single-threaded oracle over a token sample of the same step (the oracle is
     test infrastructure; here it is the reported CPU baseline, never the product)."""
@@ -366,6 +392,8 @@ def main():
     ap.add_argument("--reduction", choices=["sequential", "wide"], default="sequential")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-copy-ref", action="store_true",
+                    help="skip the size-matched device-to-device copy reference per op")
     ap.add_argument("--only", default="", help="comma-separated op subset: per-op timing only (profiling)")
     ap.add_argument("--copy-mib", type=int, default=0, help="also time a device-to-device copy of this size")
     ap.add_argument("--config", choices=["c3c4", "c1", "c2", "gemv", "kv", "logits"], default="c3c4",
@@ -430,6 +458,11 @@ def main():
         per_op[name] = {"us": round(ms * 1e3, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
                         "rotating_sets": nsets}
+        if not (only or args.copy_mib or args.no_copy_ref):
+            cu = copy_reference_us(rt, nbytes, args.op_iters)
+            # the same bytes moved by a plain copy: what the memory system gives at this size
+            per_op[name]["copy_us"] = round(cu, 3)
+            per_op[name]["of_copy"] = round(cu / (ms * 1e3), 4)
     if args.copy_mib:
         n = args.copy_mib << 20
         src, dst = rt.alloc(n), rt.alloc(n)
