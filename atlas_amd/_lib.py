@@ -92,6 +92,8 @@ SIGNATURES = {
     "atlas_hip_rope_half_f32": [CTX, P, P, P, P, U32, U32, U32, U32],
     "atlas_hip_rope_half_f16": [CTX, P, P, P, P, U32, U32, U32, U32],
     "atlas_hip_rope_interleaved_f32": [CTX, P, P, P, P, U32, U32],
+    "atlas_hip_rope_half_qk_f32": [CTX, P, P, P, P, P, P, U32, U32, U32, U32, U32],
+    "atlas_hip_rope_half_qk_f16": [CTX, P, P, P, P, P, P, U32, U32, U32, U32, U32],
     "atlas_rope_tables_gemma4": [P, SZ, SZ, SZ, F, P, P, P],
     "atlas_rope_tables_llama": [P, SZ, SZ, F, P, P],
     "atlas_hip_swiglu_f32": [CTX, P, P, P, U64],

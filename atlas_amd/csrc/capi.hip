@@ -481,6 +481,32 @@ int atlas_hip_rope_half_f16(atlas_hip_ctx* ctx, const uint16_t* input, const flo
                     "rope_half_f16");
 }
 
+int atlas_hip_rope_half_qk_f32(atlas_hip_ctx* ctx, const float* q, const float* k, const float* cosine,
+                               const float* sine, float* q_out, float* k_out, uint32_t tokens, uint32_t q_heads,
+                               uint32_t k_heads, uint32_t head_dim, uint32_t rope_stride) {
+    int rc = enter(ctx);
+    if (rc || (rc = check_rope_half(ctx, q, cosine, sine, q_out, tokens, q_heads, head_dim, rope_stride)) ||
+        (rc = check_rope_half(ctx, k, cosine, sine, k_out, tokens, k_heads, head_dim, rope_stride)))
+        return rc;
+    return launched(ctx,
+                    atlas::launch_rope_half_pair_f32(ctx->stream, q, q_out, q_heads, k, k_out, k_heads, cosine, sine,
+                                                     tokens, head_dim, rope_stride),
+                    "rope_half_qk_f32");
+}
+
+int atlas_hip_rope_half_qk_f16(atlas_hip_ctx* ctx, const uint16_t* q, const uint16_t* k, const float* cosine,
+                               const float* sine, uint16_t* q_out, uint16_t* k_out, uint32_t tokens,
+                               uint32_t q_heads, uint32_t k_heads, uint32_t head_dim, uint32_t rope_stride) {
+    int rc = enter(ctx);
+    if (rc || (rc = check_rope_half(ctx, q, cosine, sine, q_out, tokens, q_heads, head_dim, rope_stride)) ||
+        (rc = check_rope_half(ctx, k, cosine, sine, k_out, tokens, k_heads, head_dim, rope_stride)))
+        return rc;
+    return launched(ctx,
+                    atlas::launch_rope_half_pair_f16(ctx->stream, q, q_out, q_heads, k, k_out, k_heads, cosine, sine,
+                                                     tokens, head_dim, rope_stride),
+                    "rope_half_qk_f16");
+}
+
 int atlas_hip_rope_interleaved_f32(atlas_hip_ctx* ctx, const float* input, const float* cosine, const float* sine,
                                    float* output, uint32_t rows, uint32_t hidden) {
     int rc = enter(ctx);

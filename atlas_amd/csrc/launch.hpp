@@ -57,6 +57,14 @@ hipError_t launch_rope_half_f32(hipStream_t stream, const float* x, const float*
 hipError_t launch_rope_half_f16(hipStream_t stream, const uint16_t* x, const float* cosine,
                                 const float* sine, uint16_t* out, uint32_t tokens, uint32_t heads,
                                 uint32_t head_dim, uint32_t rope_stride);
+// Q and K (x0: heads0 heads, x1: heads1 heads) of the same tokens in one
+// launch, sharing the cos/sin rows; heads1 = 0 rotates x0 alone.
+hipError_t launch_rope_half_pair_f32(hipStream_t stream, const float* x0, float* out0, uint32_t heads0,
+                                     const float* x1, float* out1, uint32_t heads1, const float* cosine,
+                                     const float* sine, uint32_t tokens, uint32_t head_dim, uint32_t rope_stride);
+hipError_t launch_rope_half_pair_f16(hipStream_t stream, const uint16_t* x0, uint16_t* out0, uint32_t heads0,
+                                     const uint16_t* x1, uint16_t* out1, uint32_t heads1, const float* cosine,
+                                     const float* sine, uint32_t tokens, uint32_t head_dim, uint32_t rope_stride);
 hipError_t launch_rope_interleaved_f32(hipStream_t stream, const float* x, const float* cosine,
                                        const float* sine, float* out, uint32_t rows,
                                        uint32_t hidden);

@@ -406,19 +406,13 @@ __device__ __forceinline__ void ld_tab(const float* p, float* dst) {
     }
 }
 
+// One thread's P pairs (starting at pair p) of one (token t, head) unit of a
+// [tokens, heads, head_dim] tensor; `unit` = t * heads + head.
 template <int P>
-__global__ __launch_bounds__(256) void rope_half_f32_kernel(const float* x, const float* cosine,
-                                                            const float* sine, float* out,
-                                                            uint32_t tokens, uint32_t heads,
-                                                            uint32_t head_dim, uint32_t rope_stride) {
+__device__ __forceinline__ void rope_half_f32_unit(const float* x, const float* cosine, const float* sine,
+                                                   float* out, uint64_t unit, uint32_t p, uint32_t t,
+                                                   uint32_t head_dim, uint32_t rope_stride) {
     const uint32_t half = head_dim / 2;
-    const uint32_t groups_per_unit = half / P;
-    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const uint64_t total = static_cast<uint64_t>(tokens) * heads * groups_per_unit;
-    if (i >= total) return;
-    const uint64_t unit = i / groups_per_unit;
-    const uint32_t p = static_cast<uint32_t>(i % groups_per_unit) * P;
-    const uint32_t t = static_cast<uint32_t>(unit / heads);
     const size_t base = unit * head_dim;
     float a[P], b[P], c[P], s[P];
     if constexpr (P == 4) {
@@ -452,18 +446,10 @@ __global__ __launch_bounds__(256) void rope_half_f32_kernel(const float* x, cons
 typedef uint32_t u32x4r __attribute__((ext_vector_type(4)));
 
 template <int P>
-__global__ __launch_bounds__(256) void rope_half_f16_kernel(const uint16_t* x, const float* cosine,
-                                                            const float* sine, uint16_t* out,
-                                                            uint32_t tokens, uint32_t heads,
-                                                            uint32_t head_dim, uint32_t rope_stride) {
+__device__ __forceinline__ void rope_half_f16_unit(const uint16_t* x, const float* cosine, const float* sine,
+                                                   uint16_t* out, uint64_t unit, uint32_t p, uint32_t t,
+                                                   uint32_t head_dim, uint32_t rope_stride) {
     const uint32_t half = head_dim / 2;
-    const uint32_t groups_per_unit = half / P;
-    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const uint64_t total = static_cast<uint64_t>(tokens) * heads * groups_per_unit;
-    if (i >= total) return;
-    const uint64_t unit = i / groups_per_unit;
-    const uint32_t p = static_cast<uint32_t>(i % groups_per_unit) * P;
-    const uint32_t t = static_cast<uint32_t>(unit / heads);
     const size_t base = unit * head_dim;
     uint16_t a[P], b[P];
     if constexpr (P == 8) {
@@ -609,40 +595,101 @@ hipError_t launch_qk_norm_rope_f32(hipStream_t stream, Reduction red, const floa
     return hipGetLastError();
 }
 
-hipError_t launch_rope_half_f32(hipStream_t stream, const float* x, const float* cosine,
-                                const float* sine, float* out, uint32_t tokens, uint32_t heads,
-                                uint32_t head_dim, uint32_t rope_stride) {
+// Two tensors sharing the cos/sin rows (Q and K of the same tokens): threads
+// [0, tokens*heads0*groups) rotate x0, the following ones x1; heads1 = 0
+// rotates one tensor.
+template <int P>
+__global__ __launch_bounds__(256) void rope_half_f32_kernel(const float* x0, float* out0, uint32_t heads0,
+                                                            const float* x1, float* out1, uint32_t heads1,
+                                                            const float* cosine, const float* sine, uint32_t tokens,
+                                                            uint32_t head_dim, uint32_t rope_stride) {
+    const uint32_t groups = (head_dim / 2) / P;
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t total0 = static_cast<uint64_t>(tokens) * heads0 * groups;
+    const uint64_t total1 = static_cast<uint64_t>(tokens) * heads1 * groups;
+    const bool second = i >= total0;
+    if (second && i - total0 >= total1) return;
+    const uint64_t j = second ? i - total0 : i;
+    const uint64_t unit = j / groups;
+    const uint32_t t = static_cast<uint32_t>(unit / (second ? heads1 : heads0));
+    const uint32_t p = static_cast<uint32_t>(j - unit * groups) * P;
+    if (second)
+        rope_half_f32_unit<P>(x1, cosine, sine, out1, unit, p, t, head_dim, rope_stride);
+    else
+        rope_half_f32_unit<P>(x0, cosine, sine, out0, unit, p, t, head_dim, rope_stride);
+}
+
+template <int P>
+__global__ __launch_bounds__(256) void rope_half_f16_kernel(const uint16_t* x0, uint16_t* out0, uint32_t heads0,
+                                                            const uint16_t* x1, uint16_t* out1, uint32_t heads1,
+                                                            const float* cosine, const float* sine, uint32_t tokens,
+                                                            uint32_t head_dim, uint32_t rope_stride) {
+    const uint32_t groups = (head_dim / 2) / P;
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t total0 = static_cast<uint64_t>(tokens) * heads0 * groups;
+    const uint64_t total1 = static_cast<uint64_t>(tokens) * heads1 * groups;
+    const bool second = i >= total0;
+    if (second && i - total0 >= total1) return;
+    const uint64_t j = second ? i - total0 : i;
+    const uint64_t unit = j / groups;
+    const uint32_t t = static_cast<uint32_t>(unit / (second ? heads1 : heads0));
+    const uint32_t p = static_cast<uint32_t>(j - unit * groups) * P;
+    if (second)
+        rope_half_f16_unit<P>(x1, cosine, sine, out1, unit, p, t, head_dim, rope_stride);
+    else
+        rope_half_f16_unit<P>(x0, cosine, sine, out0, unit, p, t, head_dim, rope_stride);
+}
+
+hipError_t launch_rope_half_pair_f32(hipStream_t stream, const float* x0, float* out0, uint32_t heads0,
+                                     const float* x1, float* out1, uint32_t heads1, const float* cosine,
+                                     const float* sine, uint32_t tokens, uint32_t head_dim, uint32_t rope_stride) {
     const uint32_t half = head_dim / 2;
-    const bool vec = (half % 4) == 0 && (rope_stride % 4) == 0 && aligned(x, 16) && aligned(out, 16) &&
-                     aligned(cosine, 16) && aligned(sine, 16);
+    const bool vec = (half % 4) == 0 && (rope_stride % 4) == 0 && aligned(x0, 16) && aligned(out0, 16) &&
+                     (heads1 == 0 || (aligned(x1, 16) && aligned(out1, 16))) && aligned(cosine, 16) &&
+                     aligned(sine, 16);
     const uint32_t P = vec ? 4 : 1;
-    const uint64_t threads = static_cast<uint64_t>(tokens) * heads * (half / P);
+    const uint64_t threads = static_cast<uint64_t>(tokens) * (static_cast<uint64_t>(heads0) + heads1) * (half / P);
     const dim3 grid(static_cast<uint32_t>((threads + 255) / 256));
     if (vec)
-        hipLaunchKernelGGL((rope_half_f32_kernel<4>), grid, dim3(256), 0, stream, x, cosine, sine, out, tokens,
-                           heads, head_dim, rope_stride);
+        hipLaunchKernelGGL((rope_half_f32_kernel<4>), grid, dim3(256), 0, stream, x0, out0, heads0, x1, out1, heads1,
+                           cosine, sine, tokens, head_dim, rope_stride);
     else
-        hipLaunchKernelGGL((rope_half_f32_kernel<1>), grid, dim3(256), 0, stream, x, cosine, sine, out, tokens,
-                           heads, head_dim, rope_stride);
+        hipLaunchKernelGGL((rope_half_f32_kernel<1>), grid, dim3(256), 0, stream, x0, out0, heads0, x1, out1, heads1,
+                           cosine, sine, tokens, head_dim, rope_stride);
     return hipGetLastError();
 }
 
-hipError_t launch_rope_half_f16(hipStream_t stream, const uint16_t* x, const float* cosine,
-                                const float* sine, uint16_t* out, uint32_t tokens, uint32_t heads,
-                                uint32_t head_dim, uint32_t rope_stride) {
+hipError_t launch_rope_half_pair_f16(hipStream_t stream, const uint16_t* x0, uint16_t* out0, uint32_t heads0,
+                                     const uint16_t* x1, uint16_t* out1, uint32_t heads1, const float* cosine,
+                                     const float* sine, uint32_t tokens, uint32_t head_dim, uint32_t rope_stride) {
     const uint32_t half = head_dim / 2;
-    const bool vec = (half % 8) == 0 && (rope_stride % 4) == 0 && aligned(x, 16) && aligned(out, 16) &&
-                     aligned(cosine, 16) && aligned(sine, 16);
+    const bool vec = (half % 8) == 0 && (rope_stride % 4) == 0 && aligned(x0, 16) && aligned(out0, 16) &&
+                     (heads1 == 0 || (aligned(x1, 16) && aligned(out1, 16))) && aligned(cosine, 16) &&
+                     aligned(sine, 16);
     const uint32_t P = vec ? 8 : 1;
-    const uint64_t threads = static_cast<uint64_t>(tokens) * heads * (half / P);
+    const uint64_t threads = static_cast<uint64_t>(tokens) * (static_cast<uint64_t>(heads0) + heads1) * (half / P);
     const dim3 grid(static_cast<uint32_t>((threads + 255) / 256));
     if (vec)
-        hipLaunchKernelGGL((rope_half_f16_kernel<8>), grid, dim3(256), 0, stream, x, cosine, sine, out, tokens,
-                           heads, head_dim, rope_stride);
+        hipLaunchKernelGGL((rope_half_f16_kernel<8>), grid, dim3(256), 0, stream, x0, out0, heads0, x1, out1, heads1,
+                           cosine, sine, tokens, head_dim, rope_stride);
     else
-        hipLaunchKernelGGL((rope_half_f16_kernel<1>), grid, dim3(256), 0, stream, x, cosine, sine, out, tokens,
-                           heads, head_dim, rope_stride);
+        hipLaunchKernelGGL((rope_half_f16_kernel<1>), grid, dim3(256), 0, stream, x0, out0, heads0, x1, out1, heads1,
+                           cosine, sine, tokens, head_dim, rope_stride);
     return hipGetLastError();
+}
+
+hipError_t launch_rope_half_f32(hipStream_t stream, const float* x, const float* cosine, const float* sine,
+                                float* out, uint32_t tokens, uint32_t heads, uint32_t head_dim,
+                                uint32_t rope_stride) {
+    return launch_rope_half_pair_f32(stream, x, out, heads, nullptr, nullptr, 0, cosine, sine, tokens, head_dim,
+                                     rope_stride);
+}
+
+hipError_t launch_rope_half_f16(hipStream_t stream, const uint16_t* x, const float* cosine, const float* sine,
+                                uint16_t* out, uint32_t tokens, uint32_t heads, uint32_t head_dim,
+                                uint32_t rope_stride) {
+    return launch_rope_half_pair_f16(stream, x, out, heads, nullptr, nullptr, 0, cosine, sine, tokens, head_dim,
+                                     rope_stride);
 }
 
 hipError_t launch_rope_interleaved_f32(hipStream_t stream, const float* x, const float* cosine,

@@ -219,6 +219,12 @@ class HipRuntime:
         self._check(self.lib.atlas_hip_rope_half_f16(
             self.ctx, _ptr(x), _ptr(cos), _ptr(sin), _ptr(y), tokens, heads, head_dim, rope_stride))
 
+    # Q and K of the same tokens in one launch (the Llama decode's two rope chains, executor.rs:1120-1166)
+    def rope_half_qk(self, q, k, cos, sin, q_out, k_out, tokens, q_heads, k_heads, head_dim, rope_stride, f16=False):
+        fn = self.lib.atlas_hip_rope_half_qk_f16 if f16 else self.lib.atlas_hip_rope_half_qk_f32
+        self._check(fn(self.ctx, _ptr(q), _ptr(k), _ptr(cos), _ptr(sin), _ptr(q_out), _ptr(k_out), tokens, q_heads,
+                       k_heads, head_dim, rope_stride))
+
     def rope_interleaved(self, x, cos, sin, y, rows, hidden):
         self._check(self.lib.atlas_hip_rope_interleaved_f32(self.ctx, _ptr(x), _ptr(cos), _ptr(sin), _ptr(y), rows, hidden))
 

@@ -153,10 +153,8 @@ class ConfigOps(Ops):
                                                                        H, S.eps)),
                 "rope_half_f16_qk": (["q", "k", "cos", "sin"], {"qo": T * NH * D // 2, "ko": T * NH * D // 2},
                                      4 * T * NH * D * 2 + 2 * T * (D // 2) * 4,
-                                     lambda rt, s: (rt.rope_half_f16(s["q"], s["cos"], s["sin"], s["qo"], T, NH, D,
-                                                                     D // 2),
-                                                    rt.rope_half_f16(s["k"], s["cos"], s["sin"], s["ko"], T, NH, D,
-                                                                     D // 2))),
+                                     lambda rt, s: rt.rope_half_qk(s["q"], s["k"], s["cos"], s["sin"], s["qo"],
+                                                                   s["ko"], T, NH, NH, D, D // 2, f16=True)),
                 "swiglu_f16": (["gate", "up"], {"o": T * F // 2}, 3 * T * F * 2,
                                lambda rt, s: rt.swiglu_f16(s["gate"], s["up"], s["o"], T * F)),
             }
@@ -235,8 +233,8 @@ class ConfigOps(Ops):
                              lambda rt, s: rt.rms_norm(s["x"], s["w"], s["y"], T, H, S.eps)),
                 "rope_half_qk": (["q", "k", "cos", "sin"], {"qo": T * QH * D, "ko": T * KH * D},
                                  2 * T * (QH + KH) * D * 4 + 2 * T * (D // 2) * 4,
-                                 lambda rt, s: (rt.rope_half(s["q"], s["cos"], s["sin"], s["qo"], T, QH, D, D // 2),
-                                                rt.rope_half(s["k"], s["cos"], s["sin"], s["ko"], T, KH, D, D // 2))),
+                                 lambda rt, s: rt.rope_half_qk(s["q"], s["k"], s["cos"], s["sin"], s["qo"], s["ko"],
+                                                               T, QH, KH, D, D // 2)),
                 "swiglu": (["gate", "up"], {"o": T * F}, 3 * T * F * 4,
                            lambda rt, s: rt.swiglu(s["gate"], s["up"], s["o"], T * F)),
                 "embed_f32": (["table", "ids"], {"e": T * H}, T * H * 4 + T * 4 + T * H * 4,

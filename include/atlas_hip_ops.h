@@ -192,6 +192,16 @@ int atlas_hip_rope_half_f32(atlas_hip_ctx *ctx, const float *input, const float 
 int atlas_hip_rope_half_f16(atlas_hip_ctx *ctx, const uint16_t *input, const float *cosine,
                             const float *sine, uint16_t *output, uint32_t tokens, uint32_t heads,
                             uint32_t head_dim, uint32_t rope_stride);
+/* The Llama decode rotates Q and then K of the same tokens with the same
+ * cos/sin rows, each through the three-dispatch chain above (executor.rs:
+ * 1120-1166).  This is both tensors in one launch: q [tokens, q_heads,
+ * head_dim], k [tokens, k_heads, head_dim]; results as two rope_half calls. */
+int atlas_hip_rope_half_qk_f32(atlas_hip_ctx *ctx, const float *q, const float *k, const float *cosine,
+                               const float *sine, float *q_out, float *k_out, uint32_t tokens, uint32_t q_heads,
+                               uint32_t k_heads, uint32_t head_dim, uint32_t rope_stride);
+int atlas_hip_rope_half_qk_f16(atlas_hip_ctx *ctx, const uint16_t *q, const uint16_t *k, const float *cosine,
+                               const float *sine, uint16_t *q_out, uint16_t *k_out, uint32_t tokens,
+                               uint32_t q_heads, uint32_t k_heads, uint32_t head_dim, uint32_t rope_stride);
 /* rope_f32 (kernels.metal:940-949) = NeuralOps::rope: interleaved pairs, one
  * cos/sin row of hidden/2 shared by all rows. */
 int atlas_hip_rope_interleaved_f32(atlas_hip_ctx *ctx, const float *input, const float *cosine,

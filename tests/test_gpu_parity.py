@@ -431,3 +431,30 @@ def test_rope_half_shapes(rt, ora, f16, tokens, heads, head_dim):
     say(f"rope_half f16={f16} tokens={tokens} heads={heads} head_dim={head_dim}")
     tables = rope_tables_llama(inp["pos"], head_dim, 130000.0)
     assert_bits("rope_half", cases.rope_half_gpu(rt, inp, m, tables), cases.rope_half_oracle(ora, inp, m))
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("tokens,q_heads,k_heads,head_dim", [(2048, 32, 32, 64), (128, 9, 3, 64), (37, 4, 1, 128),
+                                                             (5, 3, 2, 96), (9, 2, 1, 6)])
+def test_rope_half_qk_one_launch(rt, ora, f16, tokens, q_heads, k_heads, head_dim):
+    """Q and K in one launch (the Llama decode's two rope chains, executor.rs:1120-1166) give
+    exactly the two single-tensor results; an unaligned K takes the scalar path for both."""
+    q_inp, qm = cases.rope_half_case(tokens, q_heads, head_dim, 130000.0, 9100 + tokens, f16)
+    k_inp, km = cases.rope_half_case(tokens, k_heads, head_dim, 130000.0, 9200 + tokens, f16)
+    say(f"rope_half_qk f16={f16} tokens={tokens} q_heads={q_heads} k_heads={k_heads} head_dim={head_dim}")
+    exp = cases.rope_half_oracle(ora, q_inp, qm) + cases.rope_half_oracle(ora, k_inp, km)
+    c, s = rope_tables_llama(q_inp["pos"], head_dim, 130000.0)
+    dt = q_inp["x"].dtype
+    item = np.dtype(dt).itemsize
+    for k_offset in (0, 1):
+        cb, sb = rt.upload(c), rt.upload(s)
+        qb = rt.upload(q_inp["x"])
+        kraw = np.zeros(k_inp["x"].size + 1, dt)
+        kraw[k_offset:k_offset + k_inp["x"].size] = k_inp["x"]
+        kb = rt.upload(kraw)
+        qo, ko = rt.empty(q_inp["x"].size, dt), rt.empty(kraw.size, dt)
+        rt.rope_half_qk(qb, kb.ptr + item * k_offset, cb, sb, qo, ko.ptr + item * k_offset, tokens, q_heads,
+                        k_heads, head_dim, head_dim // 2, f16=f16)
+        rt.sync()
+        got_k = ko.download(kraw.size, dt)[k_offset:k_offset + k_inp["x"].size]
+        assert_bits(f"rope_half_qk k_offset={k_offset}", [qo.download(q_inp["x"].size, dt), got_k], exp)
