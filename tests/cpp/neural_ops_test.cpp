@@ -16,6 +16,7 @@
 #include <string>
 #include <vector>
 
+#include "atlas_gguf.hpp"
 #include "atlas_neural_ops.hpp"
 #include "atlas_oracle.h"
 
@@ -188,10 +189,82 @@ void resident_aliased_epilogue(const atlas::NeuralOps& ops) {
     assert_bits("resident rms_residual (residual out)", dres.download(), out_exp);
 }
 
+// ---- GGUF (crates/atlas-core/tests/phase_11a_gguf.rs:99-120) -------------
+
+// GgufWriter's layout (crates/atlas-core/src/gguf.rs:237-311), restated for
+// the test: string metadata in key order, tensor infos, 32-byte aligned data.
+std::vector<uint8_t> write_gguf(const std::vector<std::pair<std::string, std::string>>& metadata,
+                                const std::string& name, const std::vector<uint64_t>& dims, uint32_t type,
+                                const std::vector<uint8_t>& data) {
+    std::vector<uint8_t> out;
+    auto u32 = [&](uint32_t v) { for (int i = 0; i < 4; ++i) out.push_back(static_cast<uint8_t>(v >> (8 * i))); };
+    auto u64 = [&](uint64_t v) { for (int i = 0; i < 8; ++i) out.push_back(static_cast<uint8_t>(v >> (8 * i))); };
+    auto str = [&](const std::string& v) { u64(v.size()); out.insert(out.end(), v.begin(), v.end()); };
+    out.insert(out.end(), {'G', 'G', 'U', 'F'});
+    u32(3);
+    u64(1);
+    u64(metadata.size());
+    for (const auto& kv : metadata) {
+        str(kv.first);
+        u32(8);
+        str(kv.second);
+    }
+    str(name);
+    u32(static_cast<uint32_t>(dims.size()));
+    for (uint64_t d : dims) u64(d);
+    u32(type);
+    u64(0);
+    while (out.size() % 32) out.push_back(0);
+    out.insert(out.end(), data.begin(), data.end());
+    return out;
+}
+
+void gguf_reader() {
+    // writer_and_reader_preserve_aligned_packed_tensors
+    std::vector<uint8_t> q4(32 * 18);
+    for (size_t i = 0; i < q4.size(); ++i) q4[i] = static_cast<uint8_t>(i * 7 + 3);
+    const auto bytes = write_gguf({{"general.alignment", "32"}, {"general.architecture", "llama"},
+                                   {"llama.block_count", "1"}},
+                                  "blk.0.attn_q.weight", {32, 32}, 2, q4);
+    try {
+        const atlas::GgufModel m = atlas::GgufModel::from_bytes(bytes);
+        if (m.metadata().at("general.architecture") != "llama") fail("gguf: architecture metadata");
+        const atlas::GgufTensor& t = m.tensor("blk.0.attn_q.weight");
+        if (t.tensor_type != atlas::GgufTensorType::Q4_0 || t.dims != std::vector<uint64_t>{32, 32})
+            fail("gguf: tensor info");
+        const auto data = m.tensor_data(t);
+        if (data.second != 32 * 18 || std::memcmp(data.first, q4.data(), q4.size()) != 0) fail("gguf: tensor data");
+    } catch (const std::exception& e) {
+        fail(std::string("gguf: valid file rejected: ") + e.what());
+    }
+    // malformed_gguf_is_rejected_before_tensor_access
+    expect_invalid("truncated GGUF header", [] { atlas::GgufModel::from_bytes({'G', 'G', 'U', 'F', 3, 0, 0, 0}); });
+    auto bad_align = write_gguf({{"general.alignment", "64"}}, "t", {32}, 2, std::vector<uint8_t>(18));
+    expect_invalid("GGUF alignment 64", [&] { atlas::GgufModel::from_bytes(bad_align); });
+    auto q4_1 = write_gguf({}, "t", {32}, 3, std::vector<uint8_t>(20));
+    expect_invalid("GGUF tensor type Q4_1", [&] { atlas::GgufModel::from_bytes(q4_1); });
+    expect_invalid("missing GGUF file", [] { atlas::GgufModel::open("/nonexistent/model.gguf"); });
+}
+
+// argmax_reduction_preserves_large_vocabulary_and_highest_tie
+// (crates/atlas-metal/src/lib.rs:2217-2230), through the device entry point.
+void argmax_known_answer(const atlas::NeuralOps& ops) {
+    std::vector<float> values(65537, -10.0f);
+    values[7] = 3.5f;
+    values[31111] = 9.0f;
+    values[65536] = 9.0f;
+    atlas::DeviceBuffer<float> dv(ops, values);
+    atlas::DeviceBuffer<uint32_t> sel(ops, 1);
+    ops.check(atlas_hip_argmax_f32(ops.runtime(), dv.data(), sel.data(), 1, static_cast<uint32_t>(values.size())));
+    ops.finish();
+    if (sel.download()[0] != 65536) fail("argmax: the later of two equal maxima must win");
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
     const bool require_device = argc > 1 && std::strcmp(argv[1], "--require-device") == 0;
+    gguf_reader();  // host only: runs with or without a device
     // require_ops (phase_02_operators.rs:8-19)
     atlas::NeuralOps* ops = nullptr;
     try {
@@ -199,7 +272,7 @@ int main(int argc, char** argv) {
     } catch (const atlas::OperatorError& e) {
         if (e.kind() == atlas::ErrorKind::NoDevice) {
             std::fprintf(stderr, "skipping GPU operator assertions: no HIP device is available to this process\n");
-            return require_device ? 2 : 0;
+            return require_device ? 2 : (failures ? 1 : 0);
         }
         std::fprintf(stderr, "operators should initialize: %s\n", e.what());
         return 1;
@@ -210,6 +283,7 @@ int main(int argc, char** argv) {
         bit_exact_against_oracle(*ops);
         invalid_inputs(*ops);
         resident_aliased_epilogue(*ops);
+        argmax_known_answer(*ops);
     } catch (const std::exception& e) {
         fail(std::string("unexpected exception: ") + e.what());
     }

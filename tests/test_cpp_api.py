@@ -2,7 +2,10 @@
 program tests/cpp/neural_ops_test (built by __graft_entry__.build()):
 the reference's NeuralOps known answers and tolerances
 (crates/atlas-ops/tests/phase_02_operators.rs), bit-exact checks against the
-oracle, the InvalidInput predicates and one resident call."""
+oracle, the InvalidInput predicates, one resident call, the argmax tie KAT
+(crates/atlas-metal/src/lib.rs:2217-2230), and the C++ GgufModel
+(include/atlas_gguf.hpp) on the reference's GGUF reader tests
+(crates/atlas-core/tests/phase_11a_gguf.rs:99-120), which need no device."""
 import os
 import subprocess
 
