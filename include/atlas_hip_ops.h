@@ -365,6 +365,11 @@ int atlas_hip_softcap_f32(atlas_hip_ctx *ctx, const float *input, float *output,
  * of NaN selects 0.  count >= 1 (argmax_for_test, lib.rs:1623-1628). */
 int atlas_hip_argmax_f32(atlas_hip_ctx *ctx, const float *values, uint32_t *selected, uint32_t rows,
                          uint32_t count);
+/* The argmax entry points keep per-workgroup partial results in a 512 KiB
+ * workspace that atlas_hip_init allocates for the context; every call
+ * overwrites it.  Calls on one context are ordered by its stream; a caller
+ * that moves the context to another stream (atlas_hip_set_stream) between
+ * two argmax calls must synchronise in between, or the two race. */
 /* softcap_f32 followed by argmax_f32, the decode tail of
  * encode_current_token (gemma4_executor.rs:4678-4688), in one pass:
  * capped = cap * tanh(logits / cap) (may alias logits; NULL skips the
