@@ -640,9 +640,139 @@ __global__ __launch_bounds__(256) void rope_half_f16_kernel(const uint16_t* x0, 
         rope_half_f16_unit<P>(x0, cosine, sine, out0, unit, p, t, head_dim, rope_stride);
 }
 
+// Token engine for the half-split rotation: one wavefront per token covers
+// every head of both tensors.  A head row of d elements is 2G 16-byte
+// vectors (G = (d/2)/V, V = 8 halves or 4 floats); lane l holds vector
+// c = l mod 2G of heads l/2G, l/2G + 64/2G, ..., so each load and store
+// instruction covers whole consecutive rows.  Lanes c < G hold x[p] (first
+// half), lanes c >= G hold x[p + d/2]; the partner vector sits in lane l ^ G
+// and is exchanged with one cross-lane shuffle per dword.  The token's
+// cos/sin group (pairs [(c mod G)V, +V)) is loaded once per lane and reused by
+// all its heads.  Every head's loads are issued before the first rotation
+// (NI head steps per lane, clamped to a valid head and never stored past the
+// end).  Same roundings as rope_half_f*_unit: (x0*c) - (x1*s) for the first
+// half, (x0*s) + (x1*c) for the second.
+template <bool F16, int NI>
+__global__ __launch_bounds__(256) void rope_half_token_kernel(const uint8_t* x0, uint8_t* out0, uint32_t heads0,
+                                                              const uint8_t* x1, uint8_t* out1, uint32_t heads1,
+                                                              const float* cosine, const float* sine,
+                                                              uint32_t tokens, uint32_t head_dim,
+                                                              uint32_t rope_stride, uint32_t g_shift) {
+    constexpr uint32_t V = F16 ? 8 : 4;
+    constexpr uint32_t kEsz = F16 ? 2 : 4;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= tokens) return;
+    const uint32_t G = 1u << g_shift;
+    const uint32_t c = lane & (2 * G - 1), hl = lane >> (g_shift + 1);
+    const bool first = c < G;
+    const uint32_t g = c & (G - 1);
+    const uint32_t hps = 32u >> g_shift;  // heads per step
+    const uint32_t heads = heads0 + heads1;
+    const size_t row_bytes = static_cast<size_t>(head_dim) * kEsz;
+    float cs[V], sn[V];
+    ld_tab<V>(cosine + static_cast<size_t>(t) * rope_stride + g * V, cs);
+    ld_tab<V>(sine + static_cast<size_t>(t) * rope_stride + g * V, sn);
+    auto head_offset = [&](uint32_t h, bool second) -> size_t {
+        return (second ? static_cast<size_t>(t) * heads1 + (h - heads0) : static_cast<size_t>(t) * heads0 + h) *
+                   row_bytes + c * 16u;
+    };
+    u32x4r v[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const uint32_t h = min(hl + static_cast<uint32_t>(i) * hps, heads - 1);
+        const bool second = h >= heads0;
+        v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4r*>((second ? x1 : x0) + head_offset(h, second)));
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        // partner vector: the same pairs of the other half (lane ^ G, same head)
+        const uint32_t own[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        uint32_t par[4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) par[w] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(own[w]), static_cast<int>(G), kWave));
+        const uint32_t h = hl + static_cast<uint32_t>(i) * hps;
+        if (h < heads) {
+            const bool second = h >= heads0;
+            u32x4r r;
+            uint32_t* o = reinterpret_cast<uint32_t*>(&r);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t wa = first ? own[w] : par[w], wb = first ? par[w] : own[w];
+                if constexpr (F16) {
+                    const float xa0 = h2f(static_cast<uint16_t>(wa)), xa1 = h2f(static_cast<uint16_t>(wa >> 16));
+                    const float xb0 = h2f(static_cast<uint16_t>(wb)), xb1 = h2f(static_cast<uint16_t>(wb >> 16));
+                    const float c0 = cs[2 * w], c1 = cs[2 * w + 1], s0 = sn[2 * w], s1 = sn[2 * w + 1];
+                    const float y0 = first ? xa0 * c0 - xb0 * s0 : xa0 * s0 + xb0 * c0;
+                    const float y1 = first ? xa1 * c1 - xb1 * s1 : xa1 * s1 + xb1 * c1;
+                    o[w] = static_cast<uint32_t>(f2h(y0)) | (static_cast<uint32_t>(f2h(y1)) << 16);
+                } else {
+                    const float xa = __uint_as_float(wa), xb = __uint_as_float(wb);
+                    o[w] = __float_as_uint(first ? xa * cs[w] - xb * sn[w] : xa * sn[w] + xb * cs[w]);
+                }
+            }
+            __builtin_nontemporal_store(r, reinterpret_cast<u32x4r*>((second ? out1 : out0) + head_offset(h, second)));
+        }
+    }
+}
+
+// Launches the token engine when its layout applies: 16-byte aligned
+// operands, (d/2) a multiple of the vector width with a power-of-two number
+// of vectors per head (2G <= 64), cos/sin rows on 16-byte boundaries, at
+// most 8 head steps per lane, and at least 8192 (token, head) rows.  Returns
+// false to fall back to the per-pair kernels.
+template <bool F16>
+bool launch_rope_half_token(hipStream_t stream, const void* x0, void* out0, uint32_t heads0, const void* x1,
+                            void* out1, uint32_t heads1, const float* cosine, const float* sine, uint32_t tokens,
+                            uint32_t head_dim, uint32_t rope_stride) {
+    constexpr uint32_t V = F16 ? 8 : 4;
+    const uint32_t half = head_dim / 2;
+    if (half == 0 || half % V != 0 || rope_stride % 4 != 0 || tokens == 0) return false;
+    const uint32_t G = half / V;
+    if (G > 32 || (G & (G - 1)) != 0) return false;
+    if (!aligned(x0, 16) || !aligned(out0, 16) || !aligned(cosine, 16) || !aligned(sine, 16) ||
+        (heads1 != 0 && (!aligned(x1, 16) || !aligned(out1, 16))))
+        return false;
+    const uint32_t g_shift = static_cast<uint32_t>(__builtin_ctz(G));
+    const uint32_t hps = 32u >> g_shift;
+    const uint32_t heads = heads0 + heads1;
+    if (heads == 0) return false;
+    // small batches are latency-bound and measured faster on the per-pair
+    // kernels (SmolLM2 shape, 128 tokens x 12 heads: 4.2 against 4.4 us)
+    if (static_cast<uint64_t>(tokens) * heads < 8192) return false;
+    const uint32_t ni = (heads + hps - 1) / hps;
+    const dim3 grid((tokens + 3) / 4);
+    const uint8_t* a0 = static_cast<const uint8_t*>(x0);
+    const uint8_t* a1 = static_cast<const uint8_t*>(x1);
+    uint8_t* b0 = static_cast<uint8_t*>(out0);
+    uint8_t* b1 = static_cast<uint8_t*>(out1);
+#define ATLAS_ROPE_TOKEN_CASE(N)                                                                             \
+    case N:                                                                                                  \
+        hipLaunchKernelGGL((rope_half_token_kernel<F16, N>), grid, dim3(256), 0, stream, a0, b0, heads0, a1, \
+                           b1, heads1, cosine, sine, tokens, head_dim, rope_stride, g_shift);                \
+        return true;
+    switch (ni) {
+        ATLAS_ROPE_TOKEN_CASE(1) ATLAS_ROPE_TOKEN_CASE(2) ATLAS_ROPE_TOKEN_CASE(3) ATLAS_ROPE_TOKEN_CASE(4)
+        ATLAS_ROPE_TOKEN_CASE(5) ATLAS_ROPE_TOKEN_CASE(6) ATLAS_ROPE_TOKEN_CASE(7) ATLAS_ROPE_TOKEN_CASE(8)
+        default: return false;
+    }
+#undef ATLAS_ROPE_TOKEN_CASE
+}
+
+bool rope_token_disabled() {
+    static const bool off = [] {
+        const char* v = getenv("ATLAS_ROPE_TOKEN");
+        return v && *v == '0';
+    }();
+    return off;
+}
+
 hipError_t launch_rope_half_pair_f32(hipStream_t stream, const float* x0, float* out0, uint32_t heads0,
                                      const float* x1, float* out1, uint32_t heads1, const float* cosine,
                                      const float* sine, uint32_t tokens, uint32_t head_dim, uint32_t rope_stride) {
+    if (!rope_token_disabled() && launch_rope_half_token<false>(stream, x0, out0, heads0, x1, out1, heads1, cosine,
+                                                                sine, tokens, head_dim, rope_stride))
+        return hipGetLastError();
     const uint32_t half = head_dim / 2;
     const bool vec = (half % 4) == 0 && (rope_stride % 4) == 0 && aligned(x0, 16) && aligned(out0, 16) &&
                      (heads1 == 0 || (aligned(x1, 16) && aligned(out1, 16))) && aligned(cosine, 16) &&
@@ -662,6 +792,9 @@ hipError_t launch_rope_half_pair_f32(hipStream_t stream, const float* x0, float*
 hipError_t launch_rope_half_pair_f16(hipStream_t stream, const uint16_t* x0, uint16_t* out0, uint32_t heads0,
                                      const uint16_t* x1, uint16_t* out1, uint32_t heads1, const float* cosine,
                                      const float* sine, uint32_t tokens, uint32_t head_dim, uint32_t rope_stride) {
+    if (!rope_token_disabled() && launch_rope_half_token<true>(stream, x0, out0, heads0, x1, out1, heads1, cosine,
+                                                               sine, tokens, head_dim, rope_stride))
+        return hipGetLastError();
     const uint32_t half = head_dim / 2;
     const bool vec = (half % 8) == 0 && (rope_stride % 4) == 0 && aligned(x0, 16) && aligned(out0, 16) &&
                      (heads1 == 0 || (aligned(x1, 16) && aligned(out1, 16))) && aligned(cosine, 16) &&

@@ -1,0 +1,78 @@
+// stream_floor.hip -- measurement-only streaming kernel for bench.py.
+//
+// Not part of the operator library (built into libatlas_stream_floor.so,
+// loaded only by the benchmark).  For each op the benchmark times, it
+// launches one kernel that reads the op's input bytes and writes its output
+// bytes as plain contiguous streams: 128-bit nontemporal loads and stores,
+// 256-thread workgroups, four float4 per thread.  Launched back to back on the
+// same stream with the same buffer rotation as the op, its time is what the
+// launch path and the memory system give for that many bytes at that size,
+// with no arithmetic, no reduction and no gather -- the size-matched floor the
+// op's own time is compared against.
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kThreads = 256;
+constexpr int kPer = 4;
+
+// Thread i handles float4 index j = block*1024 + k*256 + lane of both
+// streams: it loads in[j] (j < in4) and stores it to out[j] (j < out4).
+// Loads past the output's end feed a store under a data-dependent guard that
+// never holds for finite inputs, so the compiler keeps every load.
+__global__ __launch_bounds__(kThreads) void stream_floor_kernel(const f32x4* __restrict__ in, size_t in4,
+                                                                f32x4* __restrict__ out, size_t out4,
+                                                                float* __restrict__ sink) {
+    const size_t base = static_cast<size_t>(blockIdx.x) * kThreads * kPer + threadIdx.x;
+    f32x4 v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const size_t j = base + static_cast<size_t>(k) * kThreads;
+        v[k] = j < in4 ? __builtin_nontemporal_load(in + j) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const size_t j = base + static_cast<size_t>(k) * kThreads;
+        if (j < out4)
+            __builtin_nontemporal_store(v[k], out + j);
+        else if (v[k].x != v[k].x)  // NaN: never for the benchmark's zero-filled buffers
+            sink[0] = v[k].y;
+    }
+}
+
+// Launch cost alone: one-wavefront workgroups that touch no memory (the
+// guard never holds: blockDim.x is 64).
+__global__ __launch_bounds__(64) void launch_floor_kernel(float* __restrict__ sink) {
+    if (threadIdx.x == 1000u) sink[0] = 1.0f;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Enqueue one launch of `blocks` empty one-wavefront workgroups on `stream`.
+int atlas_floor_launch(void* stream, uint32_t blocks, float* sink) {
+    if (blocks == 0) return 0;
+    hipLaunchKernelGGL(launch_floor_kernel, dim3(blocks), dim3(64), 0, static_cast<hipStream_t>(stream), sink);
+    return static_cast<int>(hipGetLastError());
+}
+
+// Enqueue one floor launch on `stream` (a hipStream_t; NULL = the default
+// stream).  in_bytes / out_bytes are rounded down to whole float4; `sink` is a
+// device float.  Returns 0 or the HIP error code.
+int atlas_floor_stream(void* stream, const void* in, size_t in_bytes, void* out, size_t out_bytes, float* sink) {
+    const size_t in4 = in_bytes / 16, out4 = out_bytes / 16;
+    const size_t n4 = in4 > out4 ? in4 : out4;
+    if (n4 == 0) return 0;
+    const size_t blocks = (n4 + kThreads * kPer - 1) / (kThreads * kPer);
+    if (blocks > 0x7fffffffu) return static_cast<int>(hipErrorInvalidValue);
+    hipLaunchKernelGGL(stream_floor_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const f32x4*>(in), in4,
+                       static_cast<f32x4*>(out), out4, sink);
+    return static_cast<int>(hipGetLastError());
+}
+
+}  // extern "C"

@@ -18,6 +18,10 @@ input read once, each output written once) / the op's average launch
 duration, from HIP events on the library's stream around back-to-back
 launches.  Every op rotates over its own buffer sets -- table copies
 included -- totalling >= 1 GiB, so the 256 MB MALL cannot serve repeats.
+Each op line also carries `floor_us`: a plain streaming kernel that reads
+the op's input bytes and writes its output bytes (measurement only,
+atlas_amd/libatlas_stream_floor.so), timed the same way -- the size-matched
+floor of launch plus memory system -- and `of_floor` = floor_us / us.
 The CPU baseline is the oracle (a single-threaded C restatement of the
 reference CPU operators) timed on this host over a bounded token sample.
 
@@ -25,6 +29,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--reduction sequenti
        python bench.py --only geglu,rms_norm        (per-op timing only, for profiling)
        python bench.py --copy-mib 256               (a D2D copy of known size: the PMC
                                                       calibration kernel)
+       python bench.py --floor-sweep                (the streaming floor alone over the ops' sizes)
        python bench.py --decode                     (configs[4] batched decode, separate line)
        python bench.py --config c1|c2|gemv|kv|logits (other op configurations, per-op lines)
 """
@@ -97,6 +102,10 @@ class Ops:
     def set_bytes(self, name):
         ins, outs, _, _ = self.table[name]
         return sum(self.host[k].nbytes for k in ins) + sum(n * 4 for n in outs.values())
+
+    def out_bytes(self, name):
+        """Bytes the op writes (its output buffers are counted in f32 elements)."""
+        return sum(n * 4 for n in self.table[name][1].values())
 
     def build_sets(self, rt, names, nsets):
         """`nsets` buffer sets holding every input/output of `names`.  Set 0 is
@@ -256,30 +265,100 @@ def time_launches(rt, launch, sets, iters):
     return rt.elapsed_ms(a, b) / iters
 
 
-def copy_reference_us(rt, nbytes, iters):
-    """Size-matched memory-system reference for an op that moves `nbytes`: the
-    runtime's device-to-device copy of nbytes/2 (nbytes/2 read + nbytes/2
-    written), timed like the ops (HIP events around back-to-back launches,
-    rotating over >= 1 GiB of distinct buffers)."""
-    half = max(16, (nbytes // 2) // 16 * 16)
-    npairs = max(4, math.ceil(ROTATION_BYTES / (2 * half)))
-    pairs = [(rt.alloc(half), rt.alloc(half)) for _ in range(npairs)]
-    for src, _ in pairs:
-        rt.memset(src, 0, half)
-    for i in range(3):
-        rt.copy(pairs[i % npairs][1], pairs[i % npairs][0], half)
-    rt.sync()
-    a, b = rt.event(), rt.event()
-    rt.record(a)
-    for i in range(iters):
-        rt.copy(pairs[i % npairs][1], pairs[i % npairs][0], half)
-    rt.record(b)
-    rt.sync()
-    us = rt.elapsed_ms(a, b) / iters * 1e3
-    for src, dst in pairs:
-        rt.free(src)
-        rt.free(dst)
-    return us
+class StreamFloor:
+    """Size-matched streaming floor for an op: one launch of a plain streaming
+    kernel (atlas_amd/libatlas_stream_floor.so, measurement only) that reads
+    the op's input bytes and writes its output bytes as contiguous 128-bit
+    nontemporal streams.  Timed like the ops: HIP events on the library's
+    stream around back-to-back launches, rotating over >= 1 GiB of distinct
+    buffers.  What the launch path and the memory system give for that many
+    bytes at that size, with no arithmetic, reduction or gather."""
+
+    def __init__(self, rt):
+        import ctypes
+
+        path = os.path.join(ROOT, "atlas_amd", "libatlas_stream_floor.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
+        self.lib = ctypes.CDLL(path)
+        self.lib.atlas_floor_stream.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                                ctypes.c_size_t, ctypes.c_void_p]
+        self.lib.atlas_floor_stream.restype = ctypes.c_int
+        self.lib.atlas_floor_launch.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p]
+        self.lib.atlas_floor_launch.restype = ctypes.c_int
+        self.rt = rt
+        self.stream = rt.lib.atlas_hip_get_stream(rt.ctx)
+        self.sink = rt.alloc(256)
+
+    def us(self, in_bytes, out_bytes, iters):
+        rt = self.rt
+        ib, ob = (in_bytes + 255) // 256 * 256, (out_bytes + 255) // 256 * 256
+        per_set = ib + ob
+        nsets = max(4, math.ceil(ROTATION_BYTES / per_set))
+        pool = rt.alloc(nsets * per_set)
+        rt.memset(pool, 0, nsets * per_set)
+
+        def launch(i):
+            base = pool.ptr + (i % nsets) * per_set
+            rc = self.lib.atlas_floor_stream(self.stream, base, in_bytes, base + ib, out_bytes, self.sink.ptr)
+            if rc != 0:
+                raise RuntimeError(f"stream floor launch failed: HIP error {rc}")
+
+        for i in range(3):
+            launch(i)
+        rt.sync()
+        a, b = rt.event(), rt.event()
+        rt.record(a)
+        for i in range(iters):
+            launch(i)
+        rt.record(b)
+        rt.sync()
+        us = rt.elapsed_ms(a, b) / iters * 1e3
+        rt.free(pool)
+        return us
+
+    def launch_us(self, blocks, iters):
+        """Back-to-back launches of `blocks` empty one-wavefront workgroups."""
+        rt = self.rt
+
+        def launch():
+            rc = self.lib.atlas_floor_launch(self.stream, blocks, self.sink.ptr)
+            if rc != 0:
+                raise RuntimeError(f"launch floor failed: HIP error {rc}")
+
+        for _ in range(3):
+            launch()
+        rt.sync()
+        a, b = rt.event(), rt.event()
+        rt.record(a)
+        for _ in range(iters):
+            launch()
+        rt.record(b)
+        rt.sync()
+        return rt.elapsed_ms(a, b) / iters * 1e3
+
+
+def floor_fields(floor, nbytes, out_bytes, op_us, iters):
+    """floor_us: the size-matched streaming floor; of_floor = floor_us / op_us
+    (1.0 = the op moves its bytes as fast as a plain stream of the same size)."""
+    fu = floor.us(nbytes - out_bytes, out_bytes, iters)
+    return {"floor_us": round(fu, 3), "of_floor": round(fu / op_us, 4)}
+
+
+def floor_sweep(rt, iters):
+    """The floor alone over the sizes the ops move (read MB, write MB): one JSON
+    line per size, for the committed floor summary."""
+    floor = StreamFloor(rt)
+    for blocks in (256, 4096, 16384):
+        print(json.dumps({"empty_workgroups": blocks, "us": round(floor.launch_us(blocks, iters), 3)}), flush=True)
+    sizes = [(1.57, 1.57), (6.3, 6.3), (12.6, 12.6), (25.2, 0.0), (0.0, 25.2), (3.5, 25.2), (25.2, 25.2),
+             (16.8, 16.8), (42.0, 37.7), (50.3, 25.2), (67.1, 33.6), (201.3, 100.7), (171.1, 143.2)]
+    for r_mb, w_mb in sizes:
+        ib, ob = int(r_mb * 1e6) // 16 * 16, int(w_mb * 1e6) // 16 * 16
+        us = floor.us(ib, ob, iters)
+        print(json.dumps({"read_MB": r_mb, "write_MB": w_mb, "us": round(us, 3),
+                          "GB/s": round((ib + ob) / (us * 1e-6) / 1e9, 1),
+                          "frac": round((ib + ob) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
 
 
 def cpu_baseline(wl, budget_s=10.0):
@@ -390,8 +469,10 @@ def main():
     ap.add_argument("--reduction", choices=["sequential", "wide"], default="sequential")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-copy-ref", action="store_true",
-                    help="skip the size-matched device-to-device copy reference per op")
+    ap.add_argument("--no-floor", action="store_true",
+                    help="skip the size-matched streaming floor per op")
+    ap.add_argument("--floor-sweep", action="store_true",
+                    help="time the streaming floor alone over the ops' sizes (one JSON line per size)")
     ap.add_argument("--only", default="", help="comma-separated op subset: per-op timing only (profiling)")
     ap.add_argument("--copy-mib", type=int, default=0, help="also time a device-to-device copy of this size")
     ap.add_argument("--config", choices=["c3c4", "c1", "c2", "gemv", "kv", "logits"], default="c3c4",
@@ -411,6 +492,11 @@ def main():
     from atlas_amd import workloads as wl
 
     rt = HipRuntime(0, ATLAS_REDUCTION_WIDE if args.reduction == "wide" else ATLAS_REDUCTION_SEQUENTIAL)
+    if args.floor_sweep:
+        floor_sweep(rt, args.op_iters)
+        rt.close()
+        return
+    floor = None if args.no_floor else StreamFloor(rt)
     if args.decode:
         print(json.dumps(decode_bench(rt, min(args.steps, 50), min(args.warmup, 5))))
         rt.close()
@@ -433,6 +519,8 @@ def main():
             per_op[name] = {"us": round(ms * 1e3, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
                             "frac": round(gbs / HBM_PEAK_GBS, 4),
                             "tokens_per_s": round(cops.tokens / (ms * 1e-3), 1), "rotating_sets": nsets}
+            if floor is not None:
+                per_op[name].update(floor_fields(floor, nbytes, cops.out_bytes(name), ms * 1e3, args.op_iters))
         print(json.dumps({"config": args.config, "per_op": per_op}))
         rt.close()
         return
@@ -456,11 +544,9 @@ def main():
         per_op[name] = {"us": round(ms * 1e3, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
                         "rotating_sets": nsets}
-        if not (only or args.copy_mib or args.no_copy_ref):
-            cu = copy_reference_us(rt, nbytes, args.op_iters)
-            # the same bytes moved by a plain copy: what the memory system gives at this size
-            per_op[name]["copy_us"] = round(cu, 3)
-            per_op[name]["of_copy"] = round(cu / (ms * 1e3), 4)
+        if not (only or args.copy_mib or args.no_floor):
+            # the same bytes moved by a plain stream: what launch + memory give at this size
+            per_op[name].update(floor_fields(floor, nbytes, ops.out_bytes(name), ms * 1e3, args.op_iters))
     if args.copy_mib:
         n = args.copy_mib << 20
         src, dst = rt.alloc(n), rt.alloc(n)

@@ -424,9 +424,11 @@ def test_f16_norm_aliasing(rt, ora):
 
 @pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("tokens,heads,head_dim", [(2048, 32, 64), (37, 3, 128), (5, 2, 96), (9, 4, 6), (3, 1, 256),
-                                                   (11, 5, 24)])
+                                                   (11, 5, 24), (301, 40, 64), (513, 16, 128), (1025, 9, 256)])
 def test_rope_half_shapes(rt, ora, f16, tokens, heads, head_dim):
-    """Half-split RoPE: 128-bit paths (half % 4 / % 8) and the scalar path."""
+    """Half-split RoPE: the token engine (>= 8192 rows; ragged last workgroup, 1-8 head
+    steps per lane, or the per-pair fallback when a lane would need more), the 128-bit
+    per-pair paths (half % 4 / % 8) and the scalar path."""
     inp, m = cases.rope_half_case(tokens, heads, head_dim, 130000.0, 8000 + tokens + head_dim, f16)
     say(f"rope_half f16={f16} tokens={tokens} heads={heads} head_dim={head_dim}")
     tables = rope_tables_llama(inp["pos"], head_dim, 130000.0)
@@ -435,7 +437,8 @@ def test_rope_half_shapes(rt, ora, f16, tokens, heads, head_dim):
 
 @pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("tokens,q_heads,k_heads,head_dim", [(2048, 32, 32, 64), (128, 9, 3, 64), (37, 4, 1, 128),
-                                                             (5, 3, 2, 96), (9, 2, 1, 6)])
+                                                             (5, 3, 2, 96), (9, 2, 1, 6), (1023, 24, 8, 64),
+                                                             (777, 13, 5, 128)])
 def test_rope_half_qk_one_launch(rt, ora, f16, tokens, q_heads, k_heads, head_dim):
     """Q and K in one launch (the Llama decode's two rope chains, executor.rs:1120-1166) give
     exactly the two single-tensor results; an unaligned K takes the scalar path for both."""
