@@ -140,7 +140,7 @@ constexpr uint32_t kYStride = 36;
 
 // LPR lanes per output row (one row per lane group), NBT blocks per lane
 // (blocks per row <= LPR * NBT).  A workgroup owns kWaves * 64 / LPR rows.
-template <int LPR, int NBT>
+template <int LPR, int NBT, bool ONEPASS>
 __global__ __launch_bounds__(256) void q4_0_matvec_kernel(MatvecArgs a) {
     constexpr uint32_t kGroups = kWave / LPR;           // rows per wavefront
     constexpr uint32_t kRows = kWaves * kGroups;        // rows per workgroup
@@ -179,9 +179,28 @@ __global__ __launch_bounds__(256) void q4_0_matvec_kernel(MatvecArgs a) {
         wv[j] = rms ? reinterpret_cast<const f32x4*>(a.rms_weight)[c] : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
     }
 
-    // 2. this wavefront's weight rows (the dominant stream), staged into LDS
-    if (wrows) stage_tile(tile + wrow0 * row_bytes, weights + static_cast<size_t>(row0 + wrow0) * row_bytes,
-                          wrows * row_bytes, lane);
+    // 2. this wavefront's weight rows (the dominant stream), staged into LDS.
+    //    ONEPASS (16-byte aligned rows of a 16-byte multiple, at most 4 KiB
+    //    per wavefront -- four 864-byte rows): the loads land in registers
+    //    and are written to LDS only after step 3, so y = x * w and the sums
+    //    overlap the HBM round trip.  Loads and stores are unconditional, with
+    //    clamped indices: a branch around either lets the compiler merge the
+    //    registers or sink the loads to the stores, which waits for the data
+    //    before step 3.  A wavefront without rows (the tail of the last tile)
+    //    copies its tile's first row into the unused slot at row nrows.
+    const uint8_t* wsrc = weights + static_cast<size_t>(row0 + (wrows ? wrow0 : 0u)) * row_bytes;
+    const uint32_t n16 = (wrows ? wrows : 1u) * row_bytes / 16;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 w0, w1, w2, w3;
+    if constexpr (ONEPASS) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(wsrc);  // read once: nontemporal
+        w0 = __builtin_nontemporal_load(src + min(lane, n16 - 1));
+        w1 = __builtin_nontemporal_load(src + min(lane + kWave, n16 - 1));
+        w2 = __builtin_nontemporal_load(src + min(lane + 2 * kWave, n16 - 1));
+        w3 = __builtin_nontemporal_load(src + min(lane + 3 * kWave, n16 - 1));
+    } else {
+        if (wrows) stage_tile(tile + wrow0 * row_bytes, wsrc, wrows * row_bytes, lane);
+    }
 
     // 3. y = x * w (or x), the per-block sums of y (a block is 8 float4, held
     //    by 8 consecutive threads) and the sum of squares
@@ -201,6 +220,13 @@ __global__ __launch_bounds__(256) void q4_0_matvec_kernel(MatvecArgs a) {
     }
     ss = group_sum<kWave>(ss);
     if (lane == 0) partial[wave] = ss;
+    if constexpr (ONEPASS) {
+        u32x4* dst = reinterpret_cast<u32x4*>(tile + wrow0 * row_bytes);
+        dst[min(lane, n16 - 1)] = w0;
+        dst[min(lane + kWave, n16 - 1)] = w1;
+        dst[min(lane + 2 * kWave, n16 - 1)] = w2;
+        dst[min(lane + 3 * kWave, n16 - 1)] = w3;
+    }
     __syncthreads();
     float inv = 1.0f;
     if (rms) inv = inverse_rms((partial[0] + partial[1]) + (partial[2] + partial[3]), static_cast<float>(n), a.epsilon);
@@ -241,6 +267,7 @@ __global__ __launch_bounds__(256) void q4_0_matvec_kernel(MatvecArgs a) {
 
 template <int LPR, int NBT>
 hipError_t launch_lpr(hipStream_t stream, MatvecArgs a) {
+    constexpr uint32_t kGroupsL = kWave / LPR;
     constexpr uint32_t kRows = kWaves * (kWave / LPR);
     uint32_t tiles = 0;
     for (uint32_t i = 0; i < a.segments; ++i) {
@@ -249,7 +276,13 @@ hipError_t launch_lpr(hipStream_t stream, MatvecArgs a) {
     }
     const uint32_t nb = a.input_width / 32;
     const size_t lds = ((kRows * nb * kQ4Block + 15) & ~15u) + (nb * kYStride + nb + kWaves) * sizeof(float);
-    hipLaunchKernelGGL((q4_0_matvec_kernel<LPR, NBT>), dim3(tiles), dim3(kWaves * kWave), lds, stream, a);
+    const uint32_t row_bytes = nb * kQ4Block;
+    bool one_pass = row_bytes % 16 == 0 && kGroupsL * row_bytes <= 4 * kWave * 16;
+    for (uint32_t i = 0; i < a.segments; ++i) one_pass = one_pass && (reinterpret_cast<uintptr_t>(a.weights[i]) & 15) == 0;
+    if (one_pass)
+        hipLaunchKernelGGL((q4_0_matvec_kernel<LPR, NBT, true>), dim3(tiles), dim3(kWaves * kWave), lds, stream, a);
+    else
+        hipLaunchKernelGGL((q4_0_matvec_kernel<LPR, NBT, false>), dim3(tiles), dim3(kWaves * kWave), lds, stream, a);
     return hipGetLastError();
 }
 
