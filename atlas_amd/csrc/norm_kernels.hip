@@ -234,7 +234,7 @@ __device__ __forceinline__ void stg_nt(float* p, f32x4 v) {
 }
 
 
-template <int R, int J, int MODE, bool PAR>
+template <int R, int J, int MODE, bool PAR, bool STAGE>
 __global__ __launch_bounds__(64) void rms_reg_kernel(NormArgs a) {
     // Squares of R rows, (hidden/4 + 1) float4 per row.  The load phase is
     // straight-line code (rows past the end and columns past the row width
@@ -254,18 +254,30 @@ __global__ __launch_bounds__(64) void rms_reg_kernel(NormArgs a) {
     f32x4 x[R][J];
     f32x4 e[kOperand ? R : 1][kOperand ? J : 1];
     f32x4 w[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const uint32_t c = min(lane + 64u * j, nv - 1);
+    auto load_chunk = [&](int j, uint32_t zero) {
+        const uint32_t c = min(lane + 64u * j, nv - 1) + zero;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const size_t idx = static_cast<size_t>(row0 + min(static_cast<uint32_t>(r), nrows - 1)) * h + 4 * c;
             x[r][j] = ldg_nt(a.x + idx);
             if (kOperand) e[r][j] = ldg_nt(operand + idx);
         }
-    }
+    };
+    // STAGE: chunk 0 of every row in the grid is requested first; a wavefront
+    // requests its later chunks only once its chunk 0 has landed (the zero
+    // offset is produced by an instruction that waits on it), so chunk 0's
+    // in-order fold runs while the later chunks are in flight instead of
+    // after every chunk of the row has arrived together.
+#pragma unroll
+    for (int j = 0; j < (STAGE ? 1 : J); ++j) load_chunk(j, 0u);
 #pragma unroll
     for (int j = 0; j < J; ++j) w[j] = ldg(a.weight + 4 * min(lane + 64u * j, nv - 1));
+    if constexpr (STAGE) {
+        uint32_t zero;
+        __asm__ volatile("v_mov_b32 %0, 0" : "=v"(zero) : "v"(x[0][0].x));
+#pragma unroll
+        for (int j = 1; j < J; ++j) load_chunk(j, zero);
+    }
 
     float s = 0.0f;  // lane r < nrows: running sum of squares of row r
     uint32_t sb[R];  // PAR: running sums of squares (bit patterns, wave-uniform)
@@ -385,11 +397,22 @@ RegConfig pick_reg(uint32_t rows, int mode) {
 
 template <int R, int J, int MODE>
 hipError_t launch_reg_rj(hipStream_t s, const NormArgs& a, bool par) {
+    // staged loads from 2048 rows up: plain RMSNorm 10.6 -> 10.2 us and the
+    // residual epilogue 16.1 -> 15.5 us at [4096, 1536]; at decode batches
+    // (256 rows) the extra round trip before the later chunks costs more
+    // (30.2 -> 30.8 us per C5 layer).  ATLAS_NORM_STAGE (0, 1) overrides.
+    static const int forced_stage = env_int("ATLAS_NORM_STAGE", -1);
+    const bool stage = forced_stage >= 0 ? forced_stage != 0 : a.rows >= 2048;
     const size_t lds = static_cast<size_t>(R) * (a.hidden / 4 + 1) * sizeof(f32x4);
-    if (par)
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true>), dim3((a.rows + R - 1) / R), dim3(kWave), lds, s, a);
+    const dim3 grid((a.rows + R - 1) / R);
+    if (par && stage)
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, true>), grid, dim3(kWave), lds, s, a);
+    else if (par)
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false>), grid, dim3(kWave), lds, s, a);
+    else if (stage)
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, true>), grid, dim3(kWave), lds, s, a);
     else
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false>), dim3((a.rows + R - 1) / R), dim3(kWave), lds, s, a);
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, false>), grid, dim3(kWave), lds, s, a);
     return hipGetLastError();
 }
 
@@ -616,7 +639,7 @@ __device__ __forceinline__ uint32_t pack16(float lo, float hi) {
     return static_cast<uint32_t>(f2h(lo)) | (static_cast<uint32_t>(f2h(hi)) << 16);
 }
 
-template <int R, int J, bool ADD, bool PAR>
+template <int R, int J, bool ADD, bool PAR, bool STAGE>
 __global__ __launch_bounds__(64) void rms_reg_f16_kernel(const uint16_t* x, const uint16_t* residual,
                                                          const uint16_t* weight, uint16_t* residual_out,
                                                          uint16_t* out, uint32_t rows, uint32_t hidden,
@@ -631,19 +654,28 @@ __global__ __launch_bounds__(64) void rms_reg_f16_kernel(const uint16_t* x, cons
     u32x4 xv[R][J];
     u32x4 ev[ADD ? R : 1][ADD ? J : 1];
     u32x4 wv[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const uint32_t c = min(lane + 64u * j, n8 - 1);
+    auto load_chunk = [&](int j, uint32_t zero) {
+        const uint32_t c = min(lane + 64u * j, n8 - 1) + zero;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const size_t idx = static_cast<size_t>(row0 + min(static_cast<uint32_t>(r), nrows - 1)) * hidden + 8 * c;
             xv[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(x + idx));
             if (ADD) ev[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(residual + idx));
         }
-    }
+    };
+    // STAGE: chunk 0 first, the later chunks once it has landed (as in
+    // rms_reg_kernel), so the in-order fold starts with the first data
+#pragma unroll
+    for (int j = 0; j < (STAGE ? 1 : J); ++j) load_chunk(j, 0u);
 #pragma unroll
     for (int j = 0; j < J; ++j)
         wv[j] = *reinterpret_cast<const u32x4*>(weight + 8 * min(lane + 64u * j, n8 - 1));
+    if constexpr (STAGE) {
+        uint32_t zero;
+        __asm__ volatile("v_mov_b32 %0, 0" : "=v"(zero) : "v"(xv[0][0].x));
+#pragma unroll
+        for (int j = 1; j < J; ++j) load_chunk(j, zero);
+    }
 
     float s = 0.0f;
     uint32_t sb[R];  // PAR: running sums of squares (bit patterns, wave-uniform)
@@ -741,12 +773,18 @@ hipError_t launch_f16_reg_rj(hipStream_t s, const uint16_t* x, const uint16_t* r
     // FP16 rows ([2048, 2048] at C2) measured slower with the parallel fold
     // (13.8 -> 16.7 us), so the in-order fold is the default here;
     // ATLAS_NORM_PAR_FOLD=1 selects the parallel one (same bits).
+    static const int forced_stage = env_int("ATLAS_NORM_STAGE", -1);
+    const bool stage = forced_stage >= 0 ? forced_stage != 0 : rows >= 2048;
+    const dim3 grid((rows + R - 1) / R);
     if (env_int("ATLAS_NORM_PAR_FOLD", 0) == 1)
-        hipLaunchKernelGGL((rms_reg_f16_kernel<R, J, ADD, true>), dim3((rows + R - 1) / R), dim3(kWave), lds, s, x,
-                           residual, weight, residual_out, out, rows, hidden, eps);
+        hipLaunchKernelGGL((rms_reg_f16_kernel<R, J, ADD, true, false>), grid, dim3(kWave), lds, s, x, residual,
+                           weight, residual_out, out, rows, hidden, eps);
+    else if (stage)
+        hipLaunchKernelGGL((rms_reg_f16_kernel<R, J, ADD, false, true>), grid, dim3(kWave), lds, s, x, residual,
+                           weight, residual_out, out, rows, hidden, eps);
     else
-        hipLaunchKernelGGL((rms_reg_f16_kernel<R, J, ADD, false>), dim3((rows + R - 1) / R), dim3(kWave), lds, s, x,
-                           residual, weight, residual_out, out, rows, hidden, eps);
+        hipLaunchKernelGGL((rms_reg_f16_kernel<R, J, ADD, false, false>), grid, dim3(kWave), lds, s, x, residual,
+                           weight, residual_out, out, rows, hidden, eps);
     return hipGetLastError();
 }
 
@@ -770,10 +808,11 @@ template <bool ADD>
 hipError_t launch_f16_reg(hipStream_t s, const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
                           uint16_t* residual_out, uint16_t* out, uint32_t rows, uint32_t hidden, float eps) {
     const int J = static_cast<int>((hidden / 8 + 63) / 64);
-    // two rows per wavefront from 2048 rows up (two wavefronts per SIMD);
+    // one row per wavefront with staged loads from 2048 rows up (C2
+    // [2048, 2048]: 13.2 us, against 13.6 with two rows per wavefront);
     // ATLAS_REG_ROWS (1, 2) overrides for sweeps
     const int forced = env_int("ATLAS_REG_ROWS", 0);
-    if (forced == 2 || (forced != 1 && rows >= 2048))
+    if (forced == 2)
         return launch_f16_reg_r<2, ADD>(s, J, x, residual, weight, residual_out, out, rows, hidden, eps);
     return launch_f16_reg_r<1, ADD>(s, J, x, residual, weight, residual_out, out, rows, hidden, eps);
 }
