@@ -25,13 +25,17 @@
 //         low nibble of byte j, value j + 16 in its high nibble).
 // The f32 arithmetic is IEEE (correctly rounded division and sqrt).
 //
-// Layout on CDNA: one 256-thread workgroup per token.  Thread t owns values
-// t + 256p of the K and V rows; a 32-value block is exactly half a
-// wavefront, so block maxima are half-wave reductions (DPP steps and one
-// ds_swizzle) and the Q4_0 nibble pairing is an xor-16 swizzle.  The V sum
-// of squares folds in order from LDS on one lane.
+// Layout on CDNA: for kv_width 256, 512 or 1024 with 16-byte aligned rows,
+// one wavefront per token (kv_append_row_kernel, below).  Otherwise one
+// 256-thread workgroup per token: thread t owns values t + 256p of the K and
+// V rows; a 32-value block is exactly half a wavefront, so block maxima are
+// half-wave reductions (DPP steps and one ds_swizzle) and the Q4_0 nibble
+// pairing is an xor-16 swizzle.  The V sum of squares folds in order from
+// LDS on one lane in both.
 #include "device_common.hpp"
 #include "launch.hpp"
+
+#include <stdlib.h>
 
 namespace atlas {
 namespace {
@@ -171,6 +175,184 @@ __global__ __launch_bounds__(256) void kv_append_kernel(KvAppendArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Row engine: two wavefronts per token (the K row and the V row, side by
+// side), two tokens per workgroup, no workgroup barrier.  For kv_width =
+// 256 * V4 (V4 = 1, 2, 4) with 16-byte aligned rows: lane l holds values
+// [4(l + 64i), +4) of its row (16-byte nontemporal loads), so a 32-value
+// block is 8 lanes.  The V sum of squares folds in index order on lane 0 from
+// LDS while the K wavefront encodes and stores; each encoded row is
+// assembled in LDS and written with 16-byte stores (a Q8_0 / Q4_0 row of 256
+// values is 272 / 144 bytes, 16-byte aligned for every position).  Same encoders as above:
+//  * block maximum over 8 lanes: the lane's fmaxf of its 4 |v|, then
+//    quad_perm xor 1, xor 2 and row_half_mirror (fmaxf ignores NaN);
+//  * Q4_0 signed maximum: the first value of the block with |v| == max
+//    (lane order, then position in the lane), or the block's value 0;
+//  * Q4_0 nibble pairing: values j and j + 16 sit in lanes g and g + 4 of
+//    the block, exchanged with an xor-4 swizzle.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void lds_wave_handoff() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ float group8_max(float v) {
+    v = fmaxf(v, dpp_f32<0xb1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f32<0x4e>(v));   // quad_perm [2,3,0,1]
+    return fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
+}
+
+// Encode the lane's 4 values (block b = lane/8 + 8i, index 4(lane%8)) into
+// the row buffer `row` (LDS, 2-byte stores: blocks are 34 / 18 bytes).
+template <int FMT>
+__device__ __forceinline__ void encode4(const f32x4 x, uint8_t* row, uint32_t block, uint32_t g) {
+    const float v[4] = {x.x, x.y, x.z, x.w};
+    // starts from |v[0]|, not 0: an all-NaN block keeps a NaN maximum, as
+    // the half-wave fold of the per-value kernel does
+    float m = __builtin_fabsf(v[0]);
+#pragma unroll
+    for (int i = 1; i < 4; ++i) m = fmaxf(m, __builtin_fabsf(v[i]));
+    const float amax = group8_max(m);
+    uint16_t* dst = reinterpret_cast<uint16_t*>(row + block * (FMT == kKvQ8_0 ? 34u : 18u));
+    if (FMT == kKvQ8_0) {
+        const float scale = amax == 0.0f ? 0.0f : fdiv_rn(amax, 127.0f);
+        uint32_t packed = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int code = 0;
+            if (scale != 0.0f) code = static_cast<int>(roundf(fminf(fmaxf(fdiv_rn(v[i], scale), -127.0f), 127.0f)));
+            packed |= (static_cast<uint32_t>(code) & 0xffu) << (8 * i);
+        }
+        if (g == 0) dst[0] = static_cast<uint16_t>(f16_bits(scale));
+        dst[1 + 2 * g] = static_cast<uint16_t>(packed);
+        dst[2 + 2 * g] = static_cast<uint16_t>(packed >> 16);
+    } else {
+        // first value of this lane with |v| == amax (amax > 0), else value 0
+        float cand = v[0];
+        bool has = false;
+#pragma unroll
+        for (int i = 3; i >= 0; --i) {
+            const bool hit = amax > 0.0f && __builtin_fabsf(v[i]) == amax;
+            cand = hit ? v[i] : cand;
+            has = has || hit;
+        }
+        const uint64_t hits = __builtin_amdgcn_ballot_w64(has);
+        const uint32_t base = __lane_id() & ~7u;
+        const uint32_t mine = static_cast<uint32_t>(hits >> base) & 0xffu;
+        const uint32_t src = base + (mine ? static_cast<uint32_t>(__builtin_ctz(mine)) : 0u);
+        const float smax = __int_as_float(__shfl(__float_as_int(cand), static_cast<int>(src), kWave));
+        const float scale = amax == 0.0f ? 0.0f : fdiv_rn(smax, -8.0f);
+        uint32_t packed = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            int code = 0;
+            if (scale != 0.0f) {
+                const float t = fdiv_rn(v[i], scale) + 8.5f;
+                code = t >= 15.0f ? 15 : (t > 0.0f ? static_cast<int>(t) : 0);
+            }
+            packed |= static_cast<uint32_t>(code) << (8 * i);
+        }
+        // lane g < 4 of the block holds values 4g..4g+3 (low nibbles), lane
+        // g + 4 the values 16 + 4g.. (high nibbles): xor-4 swizzle
+        const uint32_t partner = static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(packed), 0x101f));
+        if (g == 0) dst[0] = static_cast<uint16_t>(f16_bits(scale));
+        if (g < 4) {
+            const uint32_t bytes = packed | (partner << 4);
+            dst[1 + 2 * g] = static_cast<uint16_t>(bytes);
+            dst[2 + 2 * g] = static_cast<uint16_t>(bytes >> 16);
+        }
+    }
+}
+
+// Write one row: f32 straight from registers, encoded rows through LDS.
+template <int FMT, int V4>
+__device__ __forceinline__ void store_row(const f32x4 (&x)[V4], uint8_t* dst, uint8_t* lds_row, uint32_t lane,
+                                          uint32_t row_bytes) {
+    if (FMT == kKvF32) {
+#pragma unroll
+        for (int i = 0; i < V4; ++i)
+            __builtin_nontemporal_store(x[i], reinterpret_cast<f32x4*>(dst) + lane + 64u * i);
+    } else {
+#pragma unroll
+        for (int i = 0; i < V4; ++i) encode4<FMT>(x[i], lds_row, lane / 8u + 8u * i, lane & 7u);
+        lds_wave_handoff();
+        const uint32_t n16 = row_bytes / 16;  // <= 68 for V4 <= 4
+        for (uint32_t u = lane; u < n16; u += kWave)
+            __builtin_nontemporal_store(reinterpret_cast<const f32x4*>(lds_row)[u], reinterpret_cast<f32x4*>(dst) + u);
+        lds_wave_handoff();  // the buffer is rewritten by the next row
+    }
+}
+
+template <int FMT, bool VNORM, int V4>
+__global__ __launch_bounds__(256) void kv_append_row_kernel(KvAppendArgs a) {
+    constexpr uint32_t kW = 256u * V4;
+    constexpr uint32_t kRowBytes = FMT == kKvF32 ? kW * 4 : (kW / 32) * (FMT == kKvQ8_0 ? 34u : 18u);
+    __shared__ __align__(16) f32x4 sq[2][VNORM ? 64 * V4 : 1];
+    __shared__ __align__(16) uint8_t rowbuf[4][FMT == kKvF32 ? 16 : kRowBytes];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+    // two wavefronts per token: the even one writes the K row, the odd one
+    // the V row (with its norm), side by side
+    const bool is_v = (wave & 1u) != 0;
+    const uint32_t t = blockIdx.x * 2 + (wave >> 1);
+    if (t >= a.tokens) return;
+    const uint32_t position = a.positions[t];
+    if (position >= a.capacity) return;
+    const f32x4* src = reinterpret_cast<const f32x4*>((is_v ? a.value : a.key) + static_cast<size_t>(t) * kW);
+    f32x4 x[V4];
+#pragma unroll
+    for (int i = 0; i < V4; ++i) x[i] = __builtin_nontemporal_load(src + lane + 64u * i);
+    uint8_t* dst = a.cache + (static_cast<size_t>(is_v ? a.capacity : 0u) + position) * kRowBytes;
+    if (VNORM && is_v) {
+        f32x4* sqw = sq[wave >> 1];
+#pragma unroll
+        for (int i = 0; i < V4; ++i)
+            sqw[lane + 64u * i] = f32x4{x[i].x * x[i].x, x[i].y * x[i].y, x[i].z * x[i].z, x[i].w * x[i].w};
+        lds_wave_handoff();
+        float s = 0.0f;
+        if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < V4; ++i) s = fold_lds_chunk(sqw + 64 * i, 64u, s);
+        }
+        const float inv = inverse_rms(readlane_f32(s, 0), static_cast<float>(kW), a.epsilon);
+#pragma unroll
+        for (int i = 0; i < V4; ++i) x[i] = f32x4{x[i].x * inv, x[i].y * inv, x[i].z * inv, x[i].w * inv};
+    }
+    store_row<FMT, V4>(x, dst, rowbuf[wave], lane, kRowBytes);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+bool kv_row_engine_disabled() {
+    static const bool off = [] {
+        const char* v = getenv("ATLAS_KV_ROW");
+        return v && *v == '0';
+    }();
+    return off;
+}
+
+template <int FMT>
+bool launch_row(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
+    const uint32_t w = a.kv_width;
+    if ((w != 256 && w != 512 && w != 1024) || !aligned16(a.key) || !aligned16(a.value) || !aligned16(a.cache))
+        return false;
+    const dim3 grid((a.tokens + 1) / 2);
+#define ATLAS_KV_ROW(V)                                                                          \
+    if (vnorm)                                                                                   \
+        hipLaunchKernelGGL((kv_append_row_kernel<FMT, true, V>), grid, dim3(256), 0, stream, a);  \
+    else                                                                                         \
+        hipLaunchKernelGGL((kv_append_row_kernel<FMT, false, V>), grid, dim3(256), 0, stream, a);
+    if (w == 256) {
+        ATLAS_KV_ROW(1)
+    } else if (w == 512) {
+        ATLAS_KV_ROW(2)
+    } else {
+        ATLAS_KV_ROW(4)
+    }
+#undef ATLAS_KV_ROW
+    return true;
+}
+
 template <int FMT, int P>
 hipError_t launch_p(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
     if (vnorm)
@@ -185,6 +367,7 @@ hipError_t launch_p(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
 // instantiation (256 -> 1 value per thread and row, 4096 -> 16).
 template <int FMT>
 hipError_t launch_fmt(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
+    if (!kv_row_engine_disabled() && launch_row<FMT>(stream, a, vnorm)) return hipGetLastError();
     const uint32_t p = (a.kv_width + kThreads - 1) / kThreads;
     if (p <= 1) return launch_p<FMT, 1>(stream, a, vnorm);
     if (p <= 2) return launch_p<FMT, 2>(stream, a, vnorm);

@@ -104,7 +104,12 @@ class Ops:
         return sum(self.host[k].nbytes for k in ins) + sum(n * 4 for n in outs.values())
 
     def out_bytes(self, name):
-        """Bytes the op writes (its output buffers are counted in f32 elements)."""
+        """Bytes the op writes: its output buffers (counted in f32 elements),
+        or `written[name]` where a buffer is larger than what one launch
+        writes (a cache) or the op writes in place."""
+        written = getattr(self, "written", {})
+        if name in written:
+            return written[name]
         return sum(n * 4 for n in self.table[name][1].values())
 
     def build_sets(self, rt, names, nsets):
@@ -213,6 +218,9 @@ class ConfigOps(Ops):
             self.table["kv_append_q4_0_vnorm_decode"] = (
                 ["k", "v", "pos1"], {"c1": 2 * cap * rows["q4_0"] // 4}, 2 * W * 4 + 4 + 2 * rows["q4_0"],
                 lambda rt, s: rt.kv_append("q4_0", s["k"], s["v"], s["c1"], W, cap, s["pos1"], 1, True, L.eps))
+            # the cache outputs are whole caches; a launch writes its tokens' rows
+            self.written = {f"kv_append_{fmt}_vnorm_T{T}": 2 * T * rows[fmt] for fmt in ("f32", "q8_0", "q4_0")}
+            self.written["kv_append_q4_0_vnorm_decode"] = 2 * rows["q4_0"]
         elif cfg == "logits":
             # the decode tail, soft cap (30) + greedy argmax
             # over the 262144-entry vocabulary: the C5 batch of 256 sequences
@@ -228,6 +236,8 @@ class ConfigOps(Ops):
                 "softcap_argmax_B1": (["l1"], {"s1": 1}, 2 * V * 4 + 4,
                                       lambda rt, s: rt.softcap_argmax(s["l1"], s["l1"], s["s1"], 1, V, cap)),
             }
+            # the soft cap rewrites the logits in place
+            self.written = {"softcap_argmax_B256": 256 * V * 4 + 256 * 4, "softcap_argmax_B1": V * 4 + 4}
         else:
             S = wl.SmolShape()
             T, H, QH, KH, D, F, V = S.tokens, S.hidden, S.q_heads, S.kv_heads, S.head_dim, S.ffn, S.vocab
@@ -341,6 +351,7 @@ class StreamFloor:
 def floor_fields(floor, nbytes, out_bytes, op_us, iters):
     """floor_us: the size-matched streaming floor; of_floor = floor_us / op_us
     (1.0 = the op moves its bytes as fast as a plain stream of the same size)."""
+    out_bytes = min(out_bytes, nbytes)
     fu = floor.us(nbytes - out_bytes, out_bytes, iters)
     return {"floor_us": round(fu, 3), "of_floor": round(fu / op_us, 4)}
 

@@ -1,6 +1,8 @@
 """GPU tests of the KV-cache append (f32, Q8_0, Q4_0; decode and batched;
 with and without the fused V RMSNorm) through the C ABI.  The whole cache is
-compared byte for byte with the CPU restatement of the Metal kernels."""
+compared byte for byte with the CPU restatement of the Metal kernels.  Widths
+256, 512 and 1024 run the row engine (two wavefronts per token); the others
+run the per-value engine (ATLAS_KV_ROW=0 forces it for every width)."""
 import sys
 
 import numpy as np
