@@ -409,6 +409,45 @@ def test_f16_norms_shapes(rt, ora, rows, hidden):
     assert_bits("f16 norms", cases.f16_norm_gpu(rt, inp, m), cases.f16_norm_oracle(ora, inp, m))
 
 
+def _adversarial_f16_rows(rows, hidden, seed):
+    """FP16 rows built to break a reordered or wave-parallel fold: squares of f16
+    values have few significant bits, so exact rounding ties are frequent; plus
+    binade crossings from tiny to large sums, subnormal and zero stretches,
+    mixed magnitudes, and inf / NaN."""
+    r = np.random.default_rng(seed)
+    x = r.standard_normal((rows, hidden)).astype(np.float16)
+    kind = np.arange(rows) % 7
+    few = np.array([0.5, 1.0, 1.5, 2.0, 2.5, 3.0, 0.75, 1.25], np.float16)
+    x[kind == 1] = r.choice(few, (int((kind == 1).sum()), hidden)) * r.choice([-1, 1], (int((kind == 1).sum()), hidden))
+    x[kind == 2] = (r.standard_normal((int((kind == 2).sum()), hidden)) * 1e-6).astype(np.float16)   # subnormal f16
+    big = kind == 3
+    x[big] = (r.standard_normal((int(big.sum()), hidden)) * np.where(r.random((int(big.sum()), hidden)) < 0.1, 3e3, 1e-2)
+              ).astype(np.float16)
+    sparse = kind == 4
+    x[sparse] = np.where(r.random((int(sparse.sum()), hidden)) < 0.05, x[sparse], np.float16(0))
+    x[kind == 5, hidden // 3] = np.float16(np.inf)
+    x[kind == 6, hidden // 2] = np.float16(np.nan)
+    return x.reshape(-1).view(np.uint16)
+
+
+@pytest.mark.parametrize("rows,hidden", [(2048 + 37, 2048), (512 + 5, 2048), (300, 4096), (77, 1536)])
+def test_f16_norm_exact_fold_adversarial_rows(rt, ora, rows, hidden):
+    """The FP16 register engine's fold (in order, or the exact wave-parallel
+    continuations under ATLAS_NORM_PAR_FOLD=1/2) against the oracle's sequential
+    sum on adversarial f16 rows, both the plain and the add+norm form."""
+    inp, m = cases.f16_norm_case(rows, hidden, 1e-5, 7100 + rows + hidden)
+    inp["x"] = _adversarial_f16_rows(rows, hidden, 7200 + hidden)
+    say(f"f16 norms adversarial rows={rows} hidden={hidden}")
+    got, exp = cases.f16_norm_gpu(rt, inp, m), cases.f16_norm_oracle(ora, inp, m)
+    for name, g, e in zip(("residual_out", "add+norm", "norm"), got, exp):
+        gf, ef = g.view(np.float16), e.view(np.float16)
+        same = (g == e) | (np.isnan(gf) & np.isnan(ef))
+        if not same.all():
+            j = int(np.nonzero(~same)[0][0])
+            raise AssertionError(f"f16 {name}: {int((~same).sum())} of {g.size} differ; first at {j}: "
+                                 f"gpu={gf[j]!r} oracle={ef[j]!r}")
+
+
 def test_f16_norm_aliasing(rt, ora):
     """residual_out == input (the pre-norm add writes the residual stream in place)."""
     rows, h = 64, 2048
