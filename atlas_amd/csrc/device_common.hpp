@@ -152,10 +152,38 @@ __device__ __forceinline__ void silu_lanes(float (&v)[N]) {
 
 // tanh-GELU with the overflow guard (kernels.metal:752-767):
 // a = c0*(x + ((c1*x)*x)*x); inf(a) -> (a > 0 ? x : 0); else (0.5*x)*(1 + tanh(a)).
+__device__ __forceinline__ float gelu_argument(float x) { return 0.7978845608f * (x + 0.044715f * x * x * x); }
+__device__ __forceinline__ float gelu_finite_f32(float x, float argument) {
+    return 0.5f * x * (1.0f + tanh_f32(argument));
+}
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
-    const float argument = 0.7978845608f * (x + 0.044715f * x * x * x);
-    const float g = 0.5f * x * (1.0f + tanh_f32(argument));
+    const float argument = gelu_argument(x);
+    const float g = gelu_finite_f32(x, argument);
     return __builtin_isinf(argument) ? (argument > 0.0f ? x : 0.0f) : g;
+}
+
+// tanh-GELU of N values held by each lane, with the bits of gelu_tanh_f32.
+// The compiler lowers gelu_tanh_f32's overflow guard to a branch per value,
+// which serialises the N exp/divide chains; here one wave-uniform test
+// replaces it: when no argument of the wavefront is infinite (every
+// |x| < ~1.9e12), the guard selects g for every value, so the straight-line
+// form runs; otherwise the guarded form runs for the whole wavefront.
+template <int N>
+__device__ __forceinline__ void gelu_lanes(float (&v)[N]) {
+    float argument[N];
+    bool overflow = false;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        argument[i] = gelu_argument(v[i]);
+        overflow = overflow || __builtin_isinf(argument[i]);
+    }
+    if (__builtin_amdgcn_ballot_w64(overflow) == 0) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = gelu_finite_f32(v[i], argument[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = gelu_tanh_f32(v[i]);
+    }
 }
 
 // 1 / sqrt(mean + eps) with the CPU operators' two roundings

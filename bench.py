@@ -372,43 +372,76 @@ def floor_sweep(rt, iters):
                           "frac": round((ib + ob) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
 
 
-def cpu_baseline(wl, budget_s=10.0):
-    """Single-threaded oracle over a token sample of the same step (the oracle is
-    test infrastructure; here it is the reported CPU baseline, never the product)."""
+def cpu_baseline(wl, budget_s=10.0, max_threads=16):
+    """The C oracle over a token sample of the same step, single-threaded and
+    then on every host core of the box's share (at most max_threads threads,
+    each on its own token slice; ctypes releases the GIL during each C call).
+    The oracle is test infrastructure; here it is the reported CPU baseline,
+    never the product."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import threading
     import oracle as ora
 
     L, Q = wl.GemmaLayerShape(), wl.QuantGatherShape()
     Ts, H, D, QH, F = 64, L.hidden, L.head_dim, L.q_heads, L.ffn
     ple_row = Q.ple_layers * Q.ple_width
-    r = wl.rng(99)
     vocab = 4096  # a gather's cost does not depend on the vocabulary size
-    q4, q6, pt = wl.q4_0_table(r, vocab, H), wl.q6_k_table(r, vocab, H), wl.q4_0_table(r, vocab, ple_row)
-    ids = wl.token_ids(r, Ts, vocab)
-    x, res, w = wl.normal(r, Ts * H), wl.normal(r, Ts * H), wl.normal(r, H, 1, 0.1)
-    q, k, qw, kw = wl.normal(r, Ts * QH * D), wl.normal(r, Ts * D), wl.normal(r, D, 1, 0.1), wl.normal(r, D, 1, 0.1)
-    c, s = ora.rope_tables_gemma4(np.arange(Ts, dtype=np.uint32), D // 2, D, L.theta_local)
-    g, u, proj = wl.normal(r, Ts * F), wl.normal(r, Ts * F), wl.normal(r, Ts * ple_row)
     scale = float(wl.f32_sqrt(H))
 
-    def step():
-        ora.embed_q4_0(q4, ids, vocab, H, scale)
-        ora.embed_q6_k(q6, ids, vocab, H, scale)
-        ora.ple(pt, ids, proj, vocab, Q.ple_layers, Q.ple_width, 16.0, float(wl.SQRT_2_RECIP))
-        ora.rms_norm(x, w, Ts, H, L.eps)
-        ora.qk_norm_rope(q, k, qw, kw, c, s, Ts, QH, True, D, D // 2, L.eps)
-        ora.rms_norm_residual(x, w, res, Ts, H, L.eps)
-        ora.geglu(g, u)
+    def make_step(seed):
+        r = wl.rng(seed)
+        q4, q6, pt = wl.q4_0_table(r, vocab, H), wl.q6_k_table(r, vocab, H), wl.q4_0_table(r, vocab, ple_row)
+        ids = wl.token_ids(r, Ts, vocab)
+        x, res, w = wl.normal(r, Ts * H), wl.normal(r, Ts * H), wl.normal(r, H, 1, 0.1)
+        q, k = wl.normal(r, Ts * QH * D), wl.normal(r, Ts * D)
+        qw, kw = wl.normal(r, D, 1, 0.1), wl.normal(r, D, 1, 0.1)
+        c, s = ora.rope_tables_gemma4(np.arange(Ts, dtype=np.uint32), D // 2, D, L.theta_local)
+        g, u, proj = wl.normal(r, Ts * F), wl.normal(r, Ts * F), wl.normal(r, Ts * ple_row)
 
-    step()
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        step()
-        reps += 1
-    el = time.perf_counter() - t0
-    return {"value": round(Ts * reps / el, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} passes of the full step over {Ts} tokens ({el:.1f} s), single-threaded C oracle "
-                      f"(-O2, -ffp-contract=off), same op list and per-token shapes (gather vocab 4096)"}
+        def step():
+            ora.embed_q4_0(q4, ids, vocab, H, scale)
+            ora.embed_q6_k(q6, ids, vocab, H, scale)
+            ora.ple(pt, ids, proj, vocab, Q.ple_layers, Q.ple_width, 16.0, float(wl.SQRT_2_RECIP))
+            ora.rms_norm(x, w, Ts, H, L.eps)
+            ora.qk_norm_rope(q, k, qw, kw, c, s, Ts, QH, True, D, D // 2, L.eps)
+            ora.rms_norm_residual(x, w, res, Ts, H, L.eps)
+            ora.geglu(g, u)
+        return step
+
+    def timed(steps):
+        """Each step function on its own thread until budget_s; tokens/s."""
+        reps, stop = [0] * len(steps), [0.0]
+        # the deadline starts when every thread has warmed up
+        start = threading.Barrier(len(steps) + 1, action=lambda: stop.__setitem__(0, time.perf_counter() + budget_s))
+
+        def work(i):
+            steps[i]()  # warm
+            start.wait()
+            while time.perf_counter() < stop[0]:
+                steps[i]()
+                reps[i] += 1
+        pool = [threading.Thread(target=work, args=(i,)) for i in range(len(steps))]
+        for t in pool:
+            t.start()
+        start.wait()
+        t0 = stop[0] - budget_s
+        for t in pool:
+            t.join()
+        el = time.perf_counter() - t0
+        return Ts * sum(reps) / el, sum(reps), el
+
+    one, reps1, el1 = timed([make_step(99)])
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    threads = max(1, min(max_threads, cores))
+    many, reps_n, el_n = timed([make_step(99 + i) for i in range(threads)]) if threads > 1 else (one, reps1, el1)
+    return {"value": round(many, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "single_thread": round(one, 1),
+            "sample": f"the full step over {Ts}-token slices, C oracle (-O2, -ffp-contract=off), same op list "
+                      f"and per-token shapes (gather vocab 4096): {reps_n} slice passes on {threads} threads "
+                      f"({el_n:.1f} s, one slice per thread); single thread {reps1} passes ({el1:.1f} s)"}
 
 
 def decode_bench(rt, steps, warmup):

@@ -251,6 +251,24 @@ def test_geglu_offset_ple_slices(rt, ora):
                     [ora.geglu_offset(gate, ple, layer * width, layers * width, width, rows)])
 
 
+def test_geglu_offset_extremes_and_scalar_shapes(rt, ora):
+    """Overflowing and infinite gates in some wavefronts (the guarded
+    GELU form) beside ordinary ones, on the 4-wide kernel (width 256) and on
+    the scalar one (width 37, offsets not divisible by 4)."""
+    r = wl.rng(24)
+    for rows, layers, width, layer in [(96, 35, 256, 3), (50, 7, 37, 5)]:
+        gate = r.uniform(-30, 30, rows * width).astype(f32)
+        gate[[3, 700, 701, rows * width * 3 // 4]] = [np.inf, -np.inf, f32(-3e13), f32(1e20)]
+        gate[rows * width - 1] = f32(-1e20)
+        ple = wl.normal(r, rows * layers * width)
+        gb, pb, ob = rt.upload(gate), rt.upload(ple), rt.empty(rows * width)
+        say(f"geglu_offset extremes rows={rows} width={width} layer={layer}")
+        rt.geglu_offset(gb, pb, ob, layer * width, layers * width, width, rows)
+        rt.sync()
+        assert_bits("geglu_offset extremes", [ob.download(rows * width)],
+                    [ora.geglu_offset(gate, ple, layer * width, layers * width, width, rows)])
+
+
 def test_groups_stable(rt, ora):
     r = wl.rng(23)
     width, groups = 256, 35 * 64
