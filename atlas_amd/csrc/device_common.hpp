@@ -303,10 +303,10 @@ __device__ __forceinline__ uint32_t wave_inclusive_scan_u32(uint32_t v) {
     return v;
 }
 
+// The same from lane `start` on (lanes before it are already folded).
 template <int S>
-__device__ __forceinline__ uint32_t fold_chunk_exact(const float (&v)[S], uint32_t sb) {
-    const uint32_t lane = __lane_id();
-    uint32_t l0 = 0;
+__device__ __forceinline__ uint32_t fold_chunk_exact_from(const float (&v)[S], uint32_t sb, uint32_t start) {
+    uint32_t l0 = start;
     while (l0 < 64) {
         const uint32_t ex = sb >> 23;  // biased exponent (NaN/inf: >= 255)
         if (ex < 27 || ex > 251) {
@@ -352,6 +352,124 @@ __device__ __forceinline__ uint32_t fold_chunk_exact(const float (&v)[S], uint32
         }
     }
     return sb;
+}
+
+template <int S>
+__device__ __forceinline__ uint32_t fold_chunk_exact(const float (&v)[S], uint32_t sb) {
+    return fold_chunk_exact_from<S>(v, sb, 0u);
+}
+
+// ---------------------------------------------------------------------------
+// The continuation with its scans computed ahead.
+//
+// A sum of squares only grows, so its binade only moves up.  fold_scan_ahead
+// computes, before the running sum is known, what fold_chunk_exact_from
+// recomputes after every binade crossing: the per-lane ulp counts, their
+// wave prefix sums and the event lanes, for the NB binades with biased
+// exponents e0 .. e0 + NB - 1 (e0 a lower bound of the running sum's
+// exponent, e.g. from an approximate sum).  Being independent of the running
+// sum, it can overlap the in-order fold that produces it.  fold_walk then
+// runs the same event loop, switching to the next binade's scan at a
+// crossing instead of recomputing it.  A sum outside those binades (or
+// outside the exponent range [27, 251]) finishes in fold_chunk_exact_from
+// from the current lane, so the result is the sequential fold's bit pattern
+// in every case.
+// ---------------------------------------------------------------------------
+template <int NB>
+struct FoldScans {
+    uint32_t inc[NB];   // lane's ulps in binade e0 + b (0 for an event lane)
+    uint32_t incl[NB];  // inclusive wave prefix sum of inc
+    uint64_t bad[NB];   // lanes that must fold in f32 (tie, out of range)
+    uint32_t e0;
+};
+
+template <int S, int NB>
+__device__ __forceinline__ FoldScans<NB> fold_scan_ahead(const float (&v)[S], uint32_t e0) {
+    FoldScans<NB> f;
+    f.e0 = e0;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        // 2^(23-E) for the binade's ulp (clamped: a binade outside [27, 251]
+        // is never walked with its scan)
+        const uint32_t ex = min(max(e0 + b, 27u), 251u);
+        const float inv_ulp = __uint_as_float((277u - ex) << 23);
+        float ulps = 0.0f, dev = 0.0f;
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+            const float q = v[i] * inv_ulp;
+            const float m = __builtin_rintf(q);
+            dev = fmaxf(dev, __builtin_fabsf(q - m));
+            ulps = ulps + m;
+        }
+        const bool bad = !(ulps < 2097152.0f) || dev == 0.5f;
+        f.inc[b] = bad ? 0u : static_cast<uint32_t>(ulps);
+        f.incl[b] = wave_inclusive_scan_u32(f.inc[b]);
+        f.bad[b] = __builtin_amdgcn_ballot_w64(bad);
+    }
+    return f;
+}
+
+// v: lane l's S consecutive addends; sb: bit pattern of the running sum
+// before them (wave-uniform).  Returns the bit pattern after all 64 * S.
+// run_lds: the same addends in LDS, lane l's at float4 (S / 4) * l, so an
+// event lane's values are read by every lane at one address (a broadcast)
+// instead of a readlane per value, whose scalar result each dependent add
+// must wait for.
+template <int S, int NB>
+__device__ __forceinline__ uint32_t fold_walk(const FoldScans<NB>& f, const float (&v)[S], uint32_t sb,
+                                              const f32x4* run_lds) {
+    static_assert(S % 4 == 0, "the LDS copy holds whole float4");
+    uint32_t l0 = 0;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const uint32_t ex = f.e0 + b;
+        if (l0 >= 64 || (sb >> 23) != ex || ex < 27 || ex > 251) continue;
+        uint32_t base = l0 ? readlane_u32(f.incl[b], l0 - 1) : 0u;
+        for (;;) {
+            const uint32_t room = 0x800000u - (sb & 0x7fffffu);  // ulps to the next power of two
+            const uint64_t ev = (__builtin_amdgcn_ballot_w64(f.incl[b] - base >= room) | f.bad[b]) & (~0ull << l0);
+            if (ev == 0) {
+                sb += readlane_u32(f.incl[b], 63) - base;
+                l0 = 64;
+                break;
+            }
+            const uint32_t lc = static_cast<uint32_t>(__builtin_ctzll(ev));
+            const uint32_t incl_lc = readlane_u32(f.incl[b], lc);
+            sb += incl_lc - readlane_u32(f.inc[b], lc) - base;  // lanes [l0, lc): same binade, exact
+            f32x4 q[S / 4];
+#pragma unroll
+            for (int k = 0; k < S / 4; ++k) q[k] = run_lds[(S / 4) * lc + k];
+            float s = __uint_as_float(sb);
+#pragma unroll
+            for (int k = 0; k < S / 4; ++k) {
+                s = s + q[k].x;
+                s = s + q[k].y;
+                s = s + q[k].z;
+                s = s + q[k].w;
+            }
+            sb = __float_as_uint(s);
+            base = incl_lc;
+            l0 = lc + 1;
+            if (l0 >= 64 || (sb >> 23) != ex) break;
+        }
+    }
+    return l0 < 64 ? fold_chunk_exact_from<S>(v, sb, l0) : sb;
+}
+
+// Sum over the 64 lanes in no particular order (an estimate: DPP row
+// shifts then row broadcasts, the total in lane 63), broadcast to all lanes.
+template <int CTRL, int ROW_MASK, bool BOUND>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, BOUND));
+}
+__device__ __forceinline__ float wave_sum_any_order_f32(float v) {
+    v += dpp_f32<0x111, 0xf, true>(v);
+    v += dpp_f32<0x112, 0xf, true>(v);
+    v += dpp_f32<0x114, 0xf, true>(v);
+    v += dpp_f32<0x118, 0xf, true>(v);
+    v += dpp_f32<0x142, 0xa, false>(v);
+    v += dpp_f32<0x143, 0xc, false>(v);
+    return readlane_f32(v, 63);
 }
 
 }  // namespace atlas

@@ -234,22 +234,74 @@ __device__ __forceinline__ void stg_nt(float* p, f32x4 v) {
 }
 
 
-template <int R, int J, int MODE, bool PAR, bool STAGE>
-__global__ __launch_bounds__(64) void rms_reg_kernel(NormArgs a) {
+// The continuation's scans (fold_scan_ahead) as the helper wavefront leaves
+// them in LDS for the folding wavefront.
+template <int NB>
+struct FoldScansLds {
+    uint32_t inc[NB][64];
+    uint32_t incl[NB][64];
+    uint64_t bad[NB];
+    uint32_t e0;
+};
+
+template <int R, int J, int MODE, bool PAR, bool STAGE, bool RUN>
+__global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
     // Squares of R rows, (hidden/4 + 1) float4 per row.  The load phase is
     // straight-line code (rows past the end and columns past the row width
     // are clamped to valid duplicate addresses and never stored), so the
     // compiler can wait for chunk j's loads alone before folding it.
     extern __shared__ f32x4 sq4[];
     constexpr bool kOperand = MODE != kNormPlain;
-    const uint32_t lane = threadIdx.x;
+    // RUN: one row; a second wavefront computes the continuation's scans
+    // (fold_scan_ahead) while the first folds the in-order head
+    constexpr bool kRun = RUN && PAR && J > 1 && R == 1;
+    constexpr int kRunS = 4 * (J > 1 ? J - 1 : 1);
+    const uint32_t lane = threadIdx.x & 63u;
     const uint32_t h = a.hidden;
     const uint32_t nv = h >> 2;
-    const uint32_t stride4 = nv + 1;
+    // RUN: a row's squares at their columns, zero-padded to 64 * J float4
+    const uint32_t stride4 = kRun ? 64u * J + 1 : nv + 1;
     const uint32_t row0 = blockIdx.x * R;
     const uint32_t nrows = min(static_cast<uint32_t>(R), a.rows - row0);
     // second operand: residual (kNormResidual, kNormAddNorm) or state (kNormAddScale)
     const float* operand = MODE == kNormAddScale ? a.out : a.residual;
+    FoldScansLds<4>* scans_lds = reinterpret_cast<FoldScansLds<4>*>(sq4 + stride4);
+    // lane l's run: the 4 * (J - 1) consecutive squares from float4 64 + (J - 1) * l
+    auto read_run = [&](float (&run)[kRunS]) {
+#pragma unroll
+        for (int i = 0; i < J - 1; ++i) {
+            const f32x4 q = sq4[64u + (J - 1) * lane + i];
+            run[4 * i] = q.x;
+            run[4 * i + 1] = q.y;
+            run[4 * i + 2] = q.z;
+            run[4 * i + 3] = q.w;
+        }
+    };
+    if constexpr (kRun) {
+        if (threadIdx.x >= 64) {  // the helper wavefront
+            __syncthreads();  // every square staged
+            const f32x4 h0 = sq4[lane];
+            const float approx = wave_sum_any_order_f32((h0.x + h0.y) + (h0.z + h0.w));
+            // any-order and in-order sums of 256 squares differ by < 3e-5
+            // relative, so this is a lower bound of the head's exponent
+            const uint32_t e0 = __float_as_uint(approx * 0.999f) >> 23;
+            float run[kRunS];
+            read_run(run);
+            const FoldScans<4> f = fold_scan_ahead<kRunS, 4>(run, e0);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                scans_lds->inc[b][lane] = f.inc[b];
+                scans_lds->incl[b][lane] = f.incl[b];
+            }
+            if (lane == 0) {
+#pragma unroll
+                for (int b = 0; b < 4; ++b) scans_lds->bad[b] = f.bad[b];
+                scans_lds->e0 = e0;
+            }
+            __syncthreads();  // scans published
+            return;
+        }
+    }
 
     f32x4 x[R][J];
     f32x4 e[kOperand ? R : 1][kOperand ? J : 1];
@@ -295,6 +347,11 @@ __global__ __launch_bounds__(64) void rms_reg_kernel(NormArgs a) {
             }
             if (!PAR || j == 0) {
                 sq4[r * stride4 + c] = f32x4{v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w};
+            } else if (kRun) {
+                // staged for the one-step continuation below (+0 past the row
+                // width: adding +0 leaves a sum of squares unchanged)
+                sq4[r * stride4 + creal] = creal < nv ? f32x4{v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w}
+                                                      : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             } else if (static_cast<uint32_t>(r) < nrows) {
                 // chunks after the first: exact wave-parallel fold (columns past
                 // the row width hold clamped duplicates and contribute +0)
@@ -304,17 +361,42 @@ __global__ __launch_bounds__(64) void rms_reg_kernel(NormArgs a) {
                 sb[r] = fold_chunk_exact<4>(sq, sb[r]);
             }
         }
-        if (!PAR || j == 0) {
+        if ((!PAR || j == 0) && !kRun) {
             __syncthreads();
             if (lane < nrows)
                 s = fold_lds_chunk(sq4 + lane * stride4 + 64u * j, min(nv, 64u * (j + 1)) - 64u * j, s);
         }
-        if (PAR && j == 0) {
+        if (PAR && !kRun && j == 0) {
             // the first chunk, where the sum crosses many binades and ties are
             // frequent, folds in order; broadcast each row's partial sum
 #pragma unroll
             for (int r = 0; r < R; ++r) sb[r] = readlane_u32(__float_as_uint(s), static_cast<uint32_t>(r));
         }
+    }
+    if constexpr (kRun) {
+        // The continuation (columns 256 .. 256 * J) as one run.  The helper
+        // wavefront computes its scans for four binades from a lower bound
+        // of the head's exponent while this one folds the head in order;
+        // the walk then has only the fold's real events (binade crossings,
+        // ties) left.
+        __syncthreads();  // every square staged
+        const float head = fold_lds_chunk(sq4, 64u, 0.0f);
+        __syncthreads();  // the helper's scans published
+        FoldScans<4> f;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            f.inc[b] = scans_lds->inc[b][lane];
+            f.incl[b] = scans_lds->incl[b][lane];
+            // readfirstlane returns int: widen through uint32_t (no sign extension)
+            const uint64_t m = scans_lds->bad[b];
+            const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(m)));
+            const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(m >> 32)));
+            f.bad[b] = static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+        }
+        f.e0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(scans_lds->e0));
+        float run[kRunS];
+        read_run(run);
+        sb[0] = fold_walk<kRunS, 4>(f, run, __float_as_uint(head), sq4 + 64);
     }
     if (MODE == kNormAddNorm) {  // stored residual stream r = x + residual
 #pragma unroll
@@ -395,6 +477,17 @@ RegConfig pick_reg(uint32_t rows, int mode) {
     return c;
 }
 
+// The continuation as one run with its scans computed ahead by a helper
+// wavefront (RUN).  Measured on MI355X: decode batches gain (C5 step at 256
+// rows: 29.5 -> 28.5 us per layer); from 2048 rows up the second wavefront
+// per row costs more than it hides ([4096, 1536]: 10.3 -> 13.9 us).
+// ATLAS_NORM_RUN (0, 1) overrides.
+bool norm_run(uint32_t rows) {
+    static const int forced = env_int("ATLAS_NORM_RUN", -1);
+    if (forced == 0 || forced == 1) return forced == 1;
+    return rows < 2048;
+}
+
 template <int R, int J, int MODE>
 hipError_t launch_reg_rj(hipStream_t s, const NormArgs& a, bool par) {
     // staged loads from 2048 rows up: plain RMSNorm 10.6 -> 10.2 us and the
@@ -403,16 +496,27 @@ hipError_t launch_reg_rj(hipStream_t s, const NormArgs& a, bool par) {
     // (30.2 -> 30.8 us per C5 layer).  ATLAS_NORM_STAGE (0, 1) overrides.
     static const int forced_stage = env_int("ATLAS_NORM_STAGE", -1);
     const bool stage = forced_stage >= 0 ? forced_stage != 0 : a.rows >= 2048;
-    const size_t lds = static_cast<size_t>(R) * (a.hidden / 4 + 1) * sizeof(f32x4);
+    const bool run = par && J > 1 && R == 1 && norm_run(a.rows);
+    const size_t lds = run ? (64u * J + 1) * sizeof(f32x4) + sizeof(FoldScansLds<4>)
+                           : static_cast<size_t>(R) * (a.hidden / 4 + 1) * sizeof(f32x4);
     const dim3 grid((a.rows + R - 1) / R);
+    if constexpr (R == 1 && J > 1) {
+        if (run) {
+            if (stage)
+                hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, true, true>), grid, dim3(2 * kWave), lds, s, a);
+            else
+                hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, true>), grid, dim3(2 * kWave), lds, s, a);
+            return hipGetLastError();
+        }
+    }
     if (par && stage)
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, true>), grid, dim3(kWave), lds, s, a);
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, true, false>), grid, dim3(kWave), lds, s, a);
     else if (par)
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false>), grid, dim3(kWave), lds, s, a);
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, false>), grid, dim3(kWave), lds, s, a);
     else if (stage)
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, true>), grid, dim3(kWave), lds, s, a);
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, true, false>), grid, dim3(kWave), lds, s, a);
     else
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, false>), grid, dim3(kWave), lds, s, a);
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, false, false>), grid, dim3(kWave), lds, s, a);
     return hipGetLastError();
 }
 

@@ -408,9 +408,11 @@ def _assert_bits_nan_equal(name, got, exp):
 def test_rms_exact_fold_adversarial_rows(rt, ora, rows, hidden, mode):
     """Both folds of the register engine against the oracle's sequential sum on
     rows built to break a reordered or wave-parallel fold.  Below 2048 rows every
-    mode uses one row per wavefront and the exact wave-parallel fold; from 2048
-    rows up, plain RMSNorm keeps the parallel fold and the epilogue modes fold in
-    order with two rows per wavefront (and a ragged tail)."""
+    mode uses one row per wavefront and the exact wave-parallel fold with its
+    scans computed ahead by a helper wavefront (the walk across binade
+    crossings, ties, subnormal, inf and NaN stretches); from 2048 rows up, plain
+    RMSNorm keeps the chunked parallel fold and the epilogue modes fold in order
+    with two rows per wavefront (and a ragged tail)."""
     inp, m = cases.rms_case(rows, hidden, 1e-6, 4000 + hidden, mode)
     inp["x"] = _adversarial_rows(rows, hidden, 5000 + hidden)
     say(f"rms exact fold adversarial {mode} rows={rows} hidden={hidden}")
