@@ -212,7 +212,11 @@ __device__ __forceinline__ uint16_t f2h(float v) {  // IEEE RNE of the f32 value
 // Sequential f32 fold of n4 (<= 64) float4 of squares from LDS into s, in
 // index order.  A full chunk is straight-line code in groups of 8 float4:
 // the next group's reads are issued before the current group's 32 adds, so
-// LDS latency hides under the dependent add chain (~8 cycles per add).
+// LDS latency hides under the dependent add chain.  The scheduling barriers
+// keep it that way: left alone, the scheduler interleaves each read just
+// one float4 ahead of its adds, and the chain then waits on LDS latency
+// (one wavefront on gfx950: 8.7 cycles per add, 6.6 with the barriers; a
+// register-fed chain is 5.6).
 __device__ __forceinline__ float fold_lds_chunk(const f32x4* p, uint32_t n4, float s) {
     if (n4 == 64) {
         f32x4 cur[8], nxt[8];
@@ -224,6 +228,7 @@ __device__ __forceinline__ float fold_lds_chunk(const f32x4* p, uint32_t n4, flo
 #pragma unroll
                 for (int i = 0; i < 8; ++i) nxt[i] = p[8 * (g + 1) + i];
             }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 s = s + cur[i].x;
@@ -231,6 +236,7 @@ __device__ __forceinline__ float fold_lds_chunk(const f32x4* p, uint32_t n4, flo
                 s = s + cur[i].z;
                 s = s + cur[i].w;
             }
+            __builtin_amdgcn_sched_barrier(0);
             if (g < 7) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
