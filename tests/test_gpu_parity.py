@@ -355,7 +355,8 @@ def test_wide_reduction_is_tolerance_level(rt, ora):
 def _adversarial_rows(rows, hidden, seed):
     """Rows that stress the exact wave-parallel fold of the sum of squares:
     rounding ties, binade crossings, zeros, subnormal and overflowing squares,
-    non-finite values and wide exponent ranges."""
+    non-finite values, wide exponent ranges and a sum that grows through many
+    binades."""
     r = np.random.default_rng(seed)
     x = r.standard_normal((rows, hidden)).astype(f32)
     for i in range(rows):
@@ -389,6 +390,10 @@ def _adversarial_rows(rows, hidden, seed):
             row *= f32(1e-6)
         elif kind == 14:
             row[:] = np.trunc(row * 64) / 64
+        elif kind == 15:
+            # squares growing geometrically 1 .. 2^16: the sum climbs past the
+            # four binades the decode-batch fold scans ahead, mid-row
+            row[:] = np.sqrt(np.exp2(np.arange(hidden) * (16.0 / hidden))).astype(f32)
     return x.reshape(-1)
 
 
