@@ -208,9 +208,71 @@ __global__ __launch_bounds__(256) void ple_quant_kernel(const uint8_t* __restric
     }
 }
 
+// The same gather-combine with one float4 per thread: workgroup
+// t * segments + s covers float4 [256 s, 256 s + 256) of token t's row and
+// stages only that segment's table bytes (1024 values: 32 Q4_0 blocks,
+// 576 B, or 4 Q6_K super-blocks, 840 B; the segment starts on a block
+// boundary).  A plain stream with one 16-byte access per thread per operand
+// measured fastest for this read/write mix on MI355X.
+template <bool Q6>
+__global__ __launch_bounds__(256) void ple_seg_kernel(const uint8_t* __restrict__ table,
+                                                      const uint32_t* __restrict__ ids,
+                                                      const float* __restrict__ projection,
+                                                      float* __restrict__ out, uint32_t vocab,
+                                                      uint32_t row_elems, uint32_t segments,
+                                                      float embedding_scale, float output_scale) {
+    __shared__ __align__(16) uint8_t seg[Q6 ? 4 * 210 : 32 * 18];
+    const uint32_t t = blockIdx.x / segments;
+    const uint32_t sg = blockIdx.x - t * segments;
+    const uint32_t n4 = row_elems / 4;
+    const uint32_t c4 = 256u * sg + threadIdx.x;
+    const size_t base = static_cast<size_t>(t) * row_elems;
+    // no early exit on the id: the projection load stays ahead of the id's
+    // round trip and the table's (an invalid id stages row 0 and skips the
+    // store, so its output stays untouched)
+    const f32x4 q = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(projection + base) + min(c4, n4 - 1));
+    const uint32_t id_raw = ids[t];
+    const bool valid = id_raw < vocab;
+    const uint32_t id = valid ? id_raw : 0u;
+    const uint32_t v0 = 1024u * sg;
+    const uint32_t seg_vals = min(1024u, row_elems - v0);
+    const uint32_t row_bytes = Q6 ? (row_elems / 256) * 210 : (row_elems / 32) * 18;
+    const uint32_t seg_off = Q6 ? (v0 / 256) * 210 : (v0 / 32) * 18;
+    const uint32_t seg_bytes = Q6 ? (seg_vals / 256) * 210 : (seg_vals / 32) * 18;
+    stage_row<1, 4, 8>(seg, table + static_cast<size_t>(id) * row_bytes + seg_off, seg_bytes, threadIdx.x,
+                       blockDim.x);
+    __syncthreads();
+    if (valid && c4 < n4) {
+        float v[4];
+        if (Q6)
+            q6_k_decode4(seg, 4 * c4 - v0, v);
+        else
+            q4_0_decode4(seg, 4 * c4 - v0, v);
+        stg_nt(out + base + 4 * c4, f32x4{(v[0] * embedding_scale + q.x) * output_scale,
+                                          (v[1] * embedding_scale + q.y) * output_scale,
+                                          (v[2] * embedding_scale + q.z) * output_scale,
+                                          (v[3] * embedding_scale + q.w) * output_scale});
+    }
+}
+
+// ATLAS_PLE_SEG=0 selects the per-token kernel below (A/B switch).
+bool ple_seg_disabled() {
+    static const bool off = [] {
+        const char* v = getenv("ATLAS_PLE_SEG");
+        return v && *v == '0';
+    }();
+    return off;
+}
+
 template <bool Q6>
 hipError_t launch_ple_it(hipStream_t stream, const uint8_t* table, const uint32_t* ids, const float* projection,
                          float* out, uint32_t vocab, uint32_t row_elems, uint32_t tokens, float es, float os) {
+    const uint32_t segments = (row_elems / 4 + 255) / 256;
+    if (!ple_seg_disabled() && static_cast<uint64_t>(tokens) * segments < (1ull << 31)) {
+        hipLaunchKernelGGL((ple_seg_kernel<Q6>), dim3(tokens * segments), dim3(256), 0, stream, table, ids,
+                           projection, out, vocab, row_elems, segments, es, os);
+        return hipGetLastError();
+    }
     const uint32_t row_bytes = Q6 ? (row_elems / 256) * 210 : (row_elems / 32) * 18;
     const size_t lds = (row_bytes + 15) & ~15u;
     const uint32_t it = (row_elems / 4 + 255) / 256;

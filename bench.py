@@ -279,7 +279,8 @@ class StreamFloor:
     """Size-matched streaming floor for an op: one launch of a plain streaming
     kernel (atlas_amd/libatlas_stream_floor.so, measurement only) that reads
     the op's input bytes and writes its output bytes as contiguous 128-bit
-    nontemporal streams.  Timed like the ops: HIP events on the library's
+    nontemporal streams, with one and with four float4 per thread; the floor
+    is the faster of the two.  Timed like the ops: HIP events on the library's
     stream around back-to-back launches, rotating over >= 1 GiB of distinct
     buffers.  What the launch path and the memory system give for that many
     bytes at that size, with no arithmetic, reduction or gather."""
@@ -291,9 +292,9 @@ class StreamFloor:
         if not os.path.exists(path):
             raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
         self.lib = ctypes.CDLL(path)
-        self.lib.atlas_floor_stream.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
-                                                ctypes.c_size_t, ctypes.c_void_p]
-        self.lib.atlas_floor_stream.restype = ctypes.c_int
+        self.lib.atlas_floor_stream_per.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                                    ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int]
+        self.lib.atlas_floor_stream_per.restype = ctypes.c_int
         self.lib.atlas_floor_launch.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p]
         self.lib.atlas_floor_launch.restype = ctypes.c_int
         self.rt = rt
@@ -301,6 +302,9 @@ class StreamFloor:
         self.sink = rt.alloc(256)
 
     def us(self, in_bytes, out_bytes, iters):
+        return min(self.us_per(in_bytes, out_bytes, iters, per) for per in (1, 4))
+
+    def us_per(self, in_bytes, out_bytes, iters, per):
         rt = self.rt
         ib, ob = (in_bytes + 255) // 256 * 256, (out_bytes + 255) // 256 * 256
         per_set = ib + ob
@@ -310,7 +314,7 @@ class StreamFloor:
 
         def launch(i):
             base = pool.ptr + (i % nsets) * per_set
-            rc = self.lib.atlas_floor_stream(self.stream, base, in_bytes, base + ib, out_bytes, self.sink.ptr)
+            rc = self.lib.atlas_floor_stream_per(self.stream, base, in_bytes, base + ib, out_bytes, self.sink.ptr, per)
             if rc != 0:
                 raise RuntimeError(f"stream floor launch failed: HIP error {rc}")
 

@@ -323,6 +323,27 @@ def test_out_of_range_ids_follow_reference(rt, ora):
     assert_bits("oob f32 zeros", [ob.download(t * h)], [ora.embed_f32(table, ids, vocab, h)])
 
 
+def test_ple_out_of_range_ids_leave_rows_untouched(rt, ora):
+    """PLE gather-combine with ids at and far past the vocabulary: those token
+    rows keep what the output held (the Q4/Q6 lookups skip them,
+    kernels.metal:655,686), the others match the oracle; a row width that is
+    not a whole number of 1024-value segments (35 x 256)."""
+    vocab, layers, width = 100, 35, 256
+    ids = np.array([1, 100, 5, 4000000000, 99, 0, 101, 50], np.uint32)
+    for q6 in (False, True):
+        inp, m = cases.ple_case(vocab, layers, width, ids.size, 630 + q6, q6)
+        inp["ids"] = ids
+        n = inp["proj"].size
+        sentinel = np.full(n, 7.0, f32)
+        say(f"ple out-of-range ids q6={q6}")
+        tb, ib, pb, ob = rt.upload(inp["table"]), rt.upload(ids), rt.upload(inp["proj"]), rt.upload(sentinel)
+        (rt.ple_q6_k if q6 else rt.ple_q4_0)(tb, ib, pb, ob, vocab, layers, width, ids.size, m["es"], m["os"])
+        rt.sync()
+        exp = ora.ple(inp["table"], ids, inp["proj"], vocab, layers, width, m["es"], m["os"], q6=q6, out=sentinel)
+        assert_bits("ple oob untouched", [ob.download(n)], [exp])
+        assert np.all(exp.reshape(ids.size, -1)[[1, 3, 6]] == 7.0)
+
+
 def test_wide_reduction_is_tolerance_level(rt, ora):
     """ATLAS_REDUCTION_WIDE reorders the sum of squares: plain RMSNorm stays
     within 1e-5 relative per element; epilogues that cancel are checked
