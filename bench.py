@@ -263,7 +263,7 @@ class ConfigOps(Ops):
 
 
 def time_launches(rt, launch, sets, iters):
-    for i in range(3):
+    for i in range(min(50, max(3, iters // 20))):
         launch(rt, sets[i % len(sets)])
     rt.sync()
     a, b = rt.event(), rt.event()
@@ -514,7 +514,9 @@ def main():
     # ~45 ms of untimed steps: clocks and memory reach steady state after a few
     # hundred launches (10 warm-up steps measured ~1.5 % lower)
     ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--op-iters", type=int, default=100)
+    # per-op timing: 1000 back-to-back launches (~50 ms at the large ops) so
+    # the average is taken at steady clocks (100 measured 1-2 % slower)
+    ap.add_argument("--op-iters", type=int, default=1000)
     ap.add_argument("--step-sets", type=int, default=4)
     ap.add_argument("--reduction", choices=["sequential", "wide"], default="sequential")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
