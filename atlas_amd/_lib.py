@@ -21,6 +21,7 @@ ATLAS_ERR_OUT_OF_MEMORY = -4
 
 ATLAS_REDUCTION_SEQUENTIAL = 0
 ATLAS_REDUCTION_WIDE = 1
+ATLAS_REDUCTION_AUTO = 2
 
 
 class DispatchTiming(ctypes.Structure):

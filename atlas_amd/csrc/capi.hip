@@ -21,7 +21,7 @@ struct atlas_hip_ctx {
     int device = 0;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
-    int reduction = ATLAS_REDUCTION_SEQUENTIAL;
+    int reduction = ATLAS_REDUCTION_AUTO;
     bool capturing = false;
     // argmax workspace (per-workgroup partial keys of the rows being
     // reduced): allocated once here, never inside an op
@@ -75,7 +75,11 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 bool fits_u32(uint64_t v) { return v <= std::numeric_limits<uint32_t>::max(); }
 
 atlas::Reduction red(const atlas_hip_ctx* ctx) {
-    return ctx->reduction == ATLAS_REDUCTION_WIDE ? atlas::kWide : atlas::kSequential;
+    switch (ctx->reduction) {
+        case ATLAS_REDUCTION_WIDE: return atlas::kWide;
+        case ATLAS_REDUCTION_AUTO: return atlas::kAuto;
+        default: return atlas::kSequential;
+    }
 }
 
 int check_norm(atlas_hip_ctx* ctx, const void* a, const void* b, const void* c, uint32_t rows,
@@ -163,7 +167,8 @@ void* atlas_hip_get_stream(atlas_hip_ctx* ctx) { return ctx ? static_cast<void*>
 
 int atlas_hip_set_reduction(atlas_hip_ctx* ctx, int reduction) {
     if (!ctx) return ATLAS_ERR_INVALID_INPUT;
-    if (reduction != ATLAS_REDUCTION_SEQUENTIAL && reduction != ATLAS_REDUCTION_WIDE)
+    if (reduction != ATLAS_REDUCTION_SEQUENTIAL && reduction != ATLAS_REDUCTION_WIDE &&
+        reduction != ATLAS_REDUCTION_AUTO)
         return invalid(ctx, "unknown reduction order");
     ctx->reduction = reduction;
     return ATLAS_OK;

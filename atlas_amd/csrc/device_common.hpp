@@ -471,6 +471,20 @@ template <int CTRL, int ROW_MASK, bool BOUND>
 __device__ __forceinline__ float dpp_f32(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xf, BOUND));
 }
+// Sum over the wavefront in a fixed tree order, the result in every lane:
+// quad_perm xor 1, xor 2, row_half_mirror, row_mirror (16-lane rows), an
+// xor-16 ds_swizzle inside each 32-lane half, then half 0 + half 1.  The
+// tolerance-level reductions (tree engines) use it; their order is fixed, so
+// repeated calls give the same bits.
+__device__ __forceinline__ float wave_sum_tree_f32(float v) {
+    v = v + dpp_f32<0xb1, 0xf, false>(v);
+    v = v + dpp_f32<0x4e, 0xf, false>(v);
+    v = v + dpp_f32<0x141, 0xf, false>(v);
+    v = v + dpp_f32<0x140, 0xf, false>(v);
+    v = v + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f));
+    return readlane_f32(v, 0) + readlane_f32(v, 32);
+}
+
 __device__ __forceinline__ float wave_sum_any_order_f32(float v) {
     v += dpp_f32<0x111, 0xf, true>(v);
     v += dpp_f32<0x112, 0xf, true>(v);

@@ -165,51 +165,9 @@ __global__ __launch_bounds__(64) void embed_quant_kernel(const uint8_t* __restri
     }
 }
 
-// PLE: one 256-thread block per token.
+// PLE gather-combine, one float4 per thread:
 //   out[t, j] = ((deq(table[id])[j] * embedding_scale) + projection[t, j]) * output_scale
-// The projection row (the dominant stream) is requested before the table row
-// is staged, IT float4 per thread, so its latency overlaps the gather.
-template <bool Q6, int IT>
-__global__ __launch_bounds__(256) void ple_quant_kernel(const uint8_t* __restrict__ table,
-                                                        const uint32_t* __restrict__ ids,
-                                                        const float* __restrict__ projection,
-                                                        float* __restrict__ out, uint32_t vocab,
-                                                        uint32_t row_elems, float embedding_scale,
-                                                        float output_scale) {
-    extern __shared__ uint8_t row[];
-    const uint32_t t = blockIdx.x;
-    const uint32_t id = ids[t];
-    if (id >= vocab) return;
-    const uint32_t n4 = row_elems / 4;
-    const size_t base = static_cast<size_t>(t) * row_elems;
-    f32x4 p[IT];
-#pragma unroll
-    for (int i = 0; i < IT; ++i) {
-        const uint32_t c4 = min(threadIdx.x + 256u * i, n4 - 1);
-        p[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(projection + base) + c4);
-    }
-    const uint32_t row_bytes = Q6 ? (row_elems / 256) * 210 : (row_elems / 32) * 18;
-    stage_row<1, 4, 8>(row, table + static_cast<size_t>(id) * row_bytes, row_bytes, threadIdx.x, blockDim.x);
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < IT; ++i) {
-        const uint32_t c4 = threadIdx.x + 256u * i;
-        if (c4 >= n4) break;
-        float v[4];
-        if (Q6)
-            q6_k_decode4(row, 4 * c4, v);
-        else
-            q4_0_decode4(row, 4 * c4, v);
-        const f32x4 q = p[i];
-        stg_nt(out + base + 4 * c4, f32x4{(v[0] * embedding_scale + q.x) * output_scale,
-                                          (v[1] * embedding_scale + q.y) * output_scale,
-                                          (v[2] * embedding_scale + q.z) * output_scale,
-                                          (v[3] * embedding_scale + q.w) * output_scale});
-    }
-}
-
-// The same gather-combine with one float4 per thread: workgroup
-// t * segments + s covers float4 [256 s, 256 s + 256) of token t's row and
+// Workgroup t * segments + s covers float4 [256 s, 256 s + 256) of token t's row and
 // stages only that segment's table bytes (1024 values: 32 Q4_0 blocks,
 // 576 B, or 4 Q6_K super-blocks, 840 B; the segment starts on a block
 // boundary).  A plain stream with one 16-byte access per thread per operand
@@ -255,41 +213,22 @@ __global__ __launch_bounds__(256) void ple_seg_kernel(const uint8_t* __restrict_
     }
 }
 
-// ATLAS_PLE_SEG=0 selects the per-token kernel below (A/B switch).
-bool ple_seg_disabled() {
-    static const bool off = [] {
-        const char* v = getenv("ATLAS_PLE_SEG");
-        return v && *v == '0';
-    }();
-    return off;
-}
-
+// One launch covers at most 2^31 - 1 workgroups; longer token ranges are
+// split into several launches over consecutive tokens.
 template <bool Q6>
 hipError_t launch_ple_it(hipStream_t stream, const uint8_t* table, const uint32_t* ids, const float* projection,
                          float* out, uint32_t vocab, uint32_t row_elems, uint32_t tokens, float es, float os) {
     const uint32_t segments = (row_elems / 4 + 255) / 256;
-    if (!ple_seg_disabled() && static_cast<uint64_t>(tokens) * segments < (1ull << 31)) {
-        hipLaunchKernelGGL((ple_seg_kernel<Q6>), dim3(tokens * segments), dim3(256), 0, stream, table, ids,
-                           projection, out, vocab, row_elems, segments, es, os);
-        return hipGetLastError();
+    const uint32_t per_launch = 0x7fffffffu / segments;
+    for (uint32_t t0 = 0; t0 < tokens; t0 += per_launch) {
+        const uint32_t n = min(per_launch, tokens - t0);
+        const size_t off = static_cast<size_t>(t0) * row_elems;
+        hipLaunchKernelGGL((ple_seg_kernel<Q6>), dim3(n * segments), dim3(256), 0, stream, table, ids + t0,
+                           projection + off, out + off, vocab, row_elems, segments, es, os);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
     }
-    const uint32_t row_bytes = Q6 ? (row_elems / 256) * 210 : (row_elems / 32) * 18;
-    const size_t lds = (row_bytes + 15) & ~15u;
-    const uint32_t it = (row_elems / 4 + 255) / 256;
-#define ATLAS_PLE_CASE(N)                                                                                    \
-    case N:                                                                                                  \
-        hipLaunchKernelGGL((ple_quant_kernel<Q6, N>), dim3(tokens), dim3(256), lds, stream, table, ids,     \
-                           projection, out, vocab, row_elems, es, os);                                       \
-        break;
-    switch (it) {
-        ATLAS_PLE_CASE(1) ATLAS_PLE_CASE(2) ATLAS_PLE_CASE(3) ATLAS_PLE_CASE(4) ATLAS_PLE_CASE(5)
-        ATLAS_PLE_CASE(6) ATLAS_PLE_CASE(7) ATLAS_PLE_CASE(8) ATLAS_PLE_CASE(9) ATLAS_PLE_CASE(10)
-        ATLAS_PLE_CASE(11) ATLAS_PLE_CASE(12) ATLAS_PLE_CASE(13) ATLAS_PLE_CASE(14) ATLAS_PLE_CASE(15)
-        ATLAS_PLE_CASE(16)
-        default: return hipErrorInvalidValue;
-    }
-#undef ATLAS_PLE_CASE
-    return hipGetLastError();
+    return hipSuccess;
 }
 
 }  // namespace

@@ -35,7 +35,6 @@
 #include "device_common.hpp"
 #include "launch.hpp"
 
-#include <stdlib.h>
 
 namespace atlas {
 namespace {
@@ -53,7 +52,8 @@ __device__ __forceinline__ int swap16(int v) { return __builtin_amdgcn_ds_swizzl
 
 // Maximum over each 32-lane half: four DPP steps inside 16-lane rows
 // (quad_perm xor 1, xor 2, row_half_mirror, row_mirror), then one swizzle.
-// fmaxf ignores NaN lanes, as the reference's max fold does.
+// fmaxf ignores NaN lanes; a half of NaN lanes only gives NaN, so the
+// encoders seed the result with 0 as the reference's fold does.
 __device__ __forceinline__ float half_wave_max(float v) {
     v = fmaxf(v, dpp_f32<0xb1>(v));
     v = fmaxf(v, dpp_f32<0x4e>(v));
@@ -68,7 +68,9 @@ __device__ __forceinline__ uint32_t f16_bits(float v) { return f2h(v); }
 // (lane % 32 = index in the block); dst points at the block's first byte.
 template <int FMT>
 __device__ __forceinline__ void encode_block(float v, uint8_t* dst, uint32_t j) {
-    const float amax = half_wave_max(__builtin_fabsf(v));
+    // maximum = max(0, |v_0|, ..., |v_31|): an all-NaN block gives 0, so its
+    // scale and codes are 0 (kernels.metal:1220-1221, 1244-1245)
+    const float amax = fmaxf(0.0f, half_wave_max(__builtin_fabsf(v)));
     if (FMT == kKvQ8_0) {
         const float scale = amax == 0.0f ? 0.0f : fdiv_rn(amax, 127.0f);
         if (j == 0) {
@@ -207,11 +209,11 @@ __device__ __forceinline__ float group8_max(float v) {
 template <int FMT>
 __device__ __forceinline__ void encode4(const f32x4 x, uint8_t* row, uint32_t block, uint32_t g) {
     const float v[4] = {x.x, x.y, x.z, x.w};
-    // starts from |v[0]|, not 0: an all-NaN block keeps a NaN maximum, as
-    // the half-wave fold of the per-value kernel does
-    float m = __builtin_fabsf(v[0]);
+    // seeded with 0, as the reference's fold is (kernels.metal:1220-1221,
+    // 1244-1245): NaN values never raise it, and an all-NaN block gives 0
+    float m = 0.0f;
 #pragma unroll
-    for (int i = 1; i < 4; ++i) m = fmaxf(m, __builtin_fabsf(v[i]));
+    for (int i = 0; i < 4; ++i) m = fmaxf(m, __builtin_fabsf(v[i]));
     const float amax = group8_max(m);
     uint16_t* dst = reinterpret_cast<uint16_t*>(row + block * (FMT == kKvQ8_0 ? 34u : 18u));
     if (FMT == kKvQ8_0) {
@@ -323,14 +325,6 @@ __global__ __launch_bounds__(256) void kv_append_row_kernel(KvAppendArgs a) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-bool kv_row_engine_disabled() {
-    static const bool off = [] {
-        const char* v = getenv("ATLAS_KV_ROW");
-        return v && *v == '0';
-    }();
-    return off;
-}
-
 template <int FMT>
 bool launch_row(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
     const uint32_t w = a.kv_width;
@@ -367,7 +361,7 @@ hipError_t launch_p(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
 // instantiation (256 -> 1 value per thread and row, 4096 -> 16).
 template <int FMT>
 hipError_t launch_fmt(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
-    if (!kv_row_engine_disabled() && launch_row<FMT>(stream, a, vnorm)) return hipGetLastError();
+    if (launch_row<FMT>(stream, a, vnorm)) return hipGetLastError();
     const uint32_t p = (a.kv_width + kThreads - 1) / kThreads;
     if (p <= 1) return launch_p<FMT, 1>(stream, a, vnorm);
     if (p <= 2) return launch_p<FMT, 2>(stream, a, vnorm);

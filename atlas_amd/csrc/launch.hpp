@@ -12,6 +12,7 @@ namespace atlas {
 enum Reduction : int {
     kSequential = 0,  // left-to-right f32 fold: bit-identical to the CPU operators
     kWide = 1,        // lane-parallel partial sums + cross-lane tree (tolerance-level)
+    kAuto = 2,        // tree for plain scaled rows, sequential where an epilogue cancels
 };
 
 // RMSNorm family (norm_kernels.hip).  Modes of the row epilogue:

@@ -27,7 +27,6 @@
 #include "device_common.hpp"
 #include "launch.hpp"
 
-#include <stdlib.h>
 
 namespace atlas {
 namespace {
@@ -205,6 +204,115 @@ __global__ __launch_bounds__(256) void rms_wide_kernel(NormArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Tree engine: the tolerance-level reduction (ATLAS_REDUCTION_AUTO for the
+// outputs that are a plain scaled row -- RMSNorm and the add-norm's y --
+// and ATLAS_REDUCTION_WIDE for every mode).  Per lane, the squares of its
+// float4 columns summed as ((a.x^2 + a.y^2) + (a.z^2 + a.w^2)) in column
+// order, then wave_sum_tree_f32; the sum differs from the sequential fold by
+// a few units in its last place, so outputs are within ~2e-6 relative of the
+// CPU operator (1e-5 is the contract).
+//
+// Structure (16-byte aligned rows, hidden <= 2048): lane l keeps float4
+// columns l + 64j (j < J) in VGPRs.  With PAIR, wavefront w owns rows w and
+// w + G (G = the grid's wavefront count, rows/2 rounded up): it issues every
+// load of both rows, then finishes row w (sum, stores) while row w + G is
+// still landing, then row w + G.  Measured on MI355X at [4096, 1536]:
+// 8.95-9.0 us, against 9.9 us with one row per wavefront and 9.3 us for a
+// plain streaming copy of the same bytes; G must be exactly rows/2 (1536 or
+// 2560 wavefronts of the same loop measured 10.3-10.9 us).  Without PAIR
+// (fewer rows), one row per wavefront.  Every row is read completely before
+// any of its outputs is written, so in-place and aliased calls are safe.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 ldg_nt(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+}
+__device__ __forceinline__ f32x4 ldg(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ void stg_nt(float* p, f32x4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+}
+
+template <int J, int MODE>
+struct TreeRow {
+    static constexpr bool kOperand = MODE != kNormPlain;
+    f32x4 x[J];
+    f32x4 e[kOperand ? J : 1];
+
+    __device__ __forceinline__ void load(const NormArgs& a, const float* operand, uint32_t row, uint32_t lane,
+                                         uint32_t nv) {
+        const size_t base = static_cast<size_t>(row) * a.hidden;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t c = min(lane + 64u * j, nv - 1);
+            x[j] = ldg_nt(a.x + base + 4 * c);
+            if (kOperand) e[j] = ldg_nt(operand + base + 4 * c);
+        }
+    }
+
+    __device__ __forceinline__ void finish(const NormArgs& a, const f32x4 (&w)[J], uint32_t row, uint32_t lane,
+                                           uint32_t nv, float scale) {
+        const size_t base = static_cast<size_t>(row) * a.hidden;
+        if (MODE == kNormAddNorm) {  // the stored residual stream r = x + residual
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const f32x4 v = x[j], b = e[j];
+                x[j] = f32x4{v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w};
+            }
+        }
+        float p = 0.0f;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const f32x4 v = x[j];
+            const float q = (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+            p = p + (lane + 64u * j < nv ? q : 0.0f);
+        }
+        const float inv = inverse_rms(wave_sum_tree_f32(p), static_cast<float>(a.hidden), a.epsilon);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t c = lane + 64u * j;
+            if (c >= nv) continue;
+            const size_t idx = base + 4 * c;
+            const f32x4 v = x[j], ww = w[j];
+            const f32x4 n{v.x * inv * ww.x, v.y * inv * ww.y, v.z * inv * ww.z, v.w * inv * ww.w};
+            if (MODE == kNormPlain) {
+                stg_nt(a.out + idx, n);
+            } else if (MODE == kNormAddNorm) {
+                stg_nt(a.residual_out + idx, v);
+                stg_nt(a.out + idx, n);
+            } else if (MODE == kNormResidual) {
+                if (a.normalized) stg_nt(a.normalized + idx, n);
+                const f32x4 b = e[j];
+                stg_nt(a.out + idx, f32x4{b.x + n.x, b.y + n.y, b.z + n.z, b.w + n.w});
+            } else {
+                const f32x4 b = e[j];
+                stg_nt(a.out + idx,
+                       f32x4{(b.x + n.x) * scale, (b.y + n.y) * scale, (b.z + n.z) * scale, (b.w + n.w) * scale});
+            }
+        }
+    }
+};
+
+template <int J, int MODE, bool PAIR>
+__global__ __launch_bounds__(256) void rms_tree_kernel(NormArgs a) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+    const uint32_t r0 = blockIdx.x * 4 + wave;
+    if (r0 >= a.rows) return;  // wavefront-uniform
+    const uint32_t r1 = r0 + gridDim.x * 4;
+    const bool second = PAIR && r1 < a.rows;
+    const uint32_t nv = a.hidden >> 2;
+    const float* operand = MODE == kNormAddScale ? a.out : a.residual;
+    TreeRow<J, MODE> row0, row1;
+    row0.load(a, operand, r0, lane, nv);
+    if (second) row1.load(a, operand, r1, lane, nv);
+    f32x4 w[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) w[j] = ldg(a.weight + 4 * min(lane + 64u * j, nv - 1));
+    const float scale = MODE == kNormAddScale ? *a.scale : 1.0f;
+    row0.finish(a, w, r0, lane, nv, scale);
+    if (second) row1.finish(a, w, r1, lane, nv, scale);
+}
+
+// ---------------------------------------------------------------------------
 // Register engine: sequential order, the default for 16-byte-aligned rows of
 // at most 2048 floats.  One wavefront owns R rows.  Lane l keeps float4
 // column c = l + 64*j (j < J) of each of its rows in registers, so HBM sees
@@ -225,15 +333,6 @@ __global__ __launch_bounds__(256) void rms_wide_kernel(NormArgs a) {
 // Each row is fully read before any of its outputs is written, so the
 // aliased bindings of the reference call sites stay valid.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ f32x4 ldg_nt(const float* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
-}
-__device__ __forceinline__ f32x4 ldg(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
-__device__ __forceinline__ void stg_nt(float* p, f32x4 v) {
-    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
-}
-
-
 // The continuation's scans (fold_scan_ahead) as the helper wavefront leaves
 // them in LDS for the folding wavefront.
 template <int NB>
@@ -244,7 +343,7 @@ struct FoldScansLds {
     uint32_t e0;
 };
 
-template <int R, int J, int MODE, bool PAR, bool STAGE, bool RUN>
+template <int R, int J, int MODE, bool PAR, bool STAGE, bool RUN, bool STRIDED = false>
 __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
     // Squares of R rows, (hidden/4 + 1) float4 per row.  The load phase is
     // straight-line code (rows past the end and columns past the row width
@@ -261,8 +360,12 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
     const uint32_t nv = h >> 2;
     // RUN: a row's squares at their columns, zero-padded to 64 * J float4
     const uint32_t stride4 = kRun ? 64u * J + 1 : nv + 1;
-    const uint32_t row0 = blockIdx.x * R;
-    const uint32_t nrows = min(static_cast<uint32_t>(R), a.rows - row0);
+    // the wavefront's rows: R consecutive rows, or (STRIDED) rows
+    // blockIdx.x + r * gridDim.x; either way the valid ones are r < nrows
+    const uint32_t row0 = STRIDED ? blockIdx.x : blockIdx.x * R;
+    const uint32_t row_step = STRIDED ? gridDim.x : 1u;
+    const uint32_t nrows = STRIDED ? min(static_cast<uint32_t>(R), (a.rows - row0 + row_step - 1) / row_step)
+                                   : min(static_cast<uint32_t>(R), a.rows - row0);
     // second operand: residual (kNormResidual, kNormAddNorm) or state (kNormAddScale)
     const float* operand = MODE == kNormAddScale ? a.out : a.residual;
     FoldScansLds<4>* scans_lds = reinterpret_cast<FoldScansLds<4>*>(sq4 + stride4);
@@ -310,7 +413,7 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
         const uint32_t c = min(lane + 64u * j, nv - 1) + zero;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const size_t idx = static_cast<size_t>(row0 + min(static_cast<uint32_t>(r), nrows - 1)) * h + 4 * c;
+            const size_t idx = static_cast<size_t>(row0 + min(static_cast<uint32_t>(r), nrows - 1) * row_step) * h + 4 * c;
             x[r][j] = ldg_nt(a.x + idx);
             if (kOperand) e[r][j] = ldg_nt(operand + idx);
         }
@@ -405,7 +508,7 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
 #pragma unroll
             for (int j = 0; j < J; ++j) {
                 const uint32_t c = lane + 64u * j;
-                if (c < nv) stg_nt(a.residual_out + static_cast<size_t>(row0 + r) * h + 4 * c, x[r][j]);
+                if (c < nv) stg_nt(a.residual_out + static_cast<size_t>(row0 + r * row_step) * h + 4 * c, x[r][j]);
             }
         }
     }
@@ -421,7 +524,7 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
         for (int j = 0; j < J; ++j) {
             const uint32_t c = lane + 64u * j;
             if (c >= nv) continue;
-            const size_t idx = static_cast<size_t>(row0 + r) * h + 4 * c;
+            const size_t idx = static_cast<size_t>(row0 + r * row_step) * h + 4 * c;
             const f32x4 v = x[r][j], ww = w[j];
             const f32x4 n{v.x * ir * ww.x, v.y * ir * ww.y, v.z * ir * ww.z, v.w * ir * ww.w};
             if (MODE == kNormPlain || MODE == kNormAddNorm) {
@@ -439,17 +542,6 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
     }
 }
 
-int env_int(const char* name, int fallback) {
-    const char* v = getenv(name);
-    if (!v || !*v) return fallback;
-    return atoi(v);
-}
-
-bool lds_engine_forced() {
-    static const bool forced = env_int("ATLAS_NORM_LDS_ENGINE", 0) != 0;
-    return forced;
-}
-
 // Register-engine configuration: rows per wavefront and the fold of the
 // chunks after the first (exact wave-parallel, or in order from LDS).  Same
 // bits either way.  Measured on MI355X:
@@ -461,51 +553,36 @@ bool lds_engine_forced() {
 //  * rows >= 2048 with an epilogue operand (residual, add-norm, add-scale):
 //    two rows per wavefront (two wavefronts per SIMD) and the in-order fold
 //    ([4096, 1536] residual: 16.0 us; one row and the parallel fold: 16.7).
-// ATLAS_REG_ROWS (1, 2, 4) and ATLAS_NORM_PAR_FOLD (0, 1) override for sweeps.
 struct RegConfig {
     int rows;
     bool par;
 };
 
 RegConfig pick_reg(uint32_t rows, int mode) {
-    static const int forced_rows = env_int("ATLAS_REG_ROWS", 0);
-    static const int forced_par = env_int("ATLAS_NORM_PAR_FOLD", -1);
-    RegConfig c{1, true};
-    if (rows >= 2048 && mode != kNormPlain) c = RegConfig{2, false};
-    if (forced_rows == 1 || forced_rows == 2 || forced_rows == 4) c.rows = forced_rows;
-    if (forced_par == 0 || forced_par == 1) c.par = forced_par == 1;
-    return c;
+    if (rows >= 2048 && mode != kNormPlain) return RegConfig{2, false};
+    return RegConfig{1, true};
 }
 
 // The continuation as one run with its scans computed ahead by a helper
 // wavefront (RUN).  Measured on MI355X: decode batches gain (C5 step at 256
 // rows: 29.5 -> 28.5 us per layer); from 2048 rows up the second wavefront
 // per row costs more than it hides ([4096, 1536]: 10.3 -> 13.9 us).
-// ATLAS_NORM_RUN (0, 1) overrides.
-bool norm_run(uint32_t rows) {
-    static const int forced = env_int("ATLAS_NORM_RUN", -1);
-    if (forced == 0 || forced == 1) return forced == 1;
-    return rows < 2048;
-}
+bool norm_run(uint32_t rows) { return rows < 2048; }
 
 template <int R, int J, int MODE>
 hipError_t launch_reg_rj(hipStream_t s, const NormArgs& a, bool par) {
     // staged loads from 2048 rows up: plain RMSNorm 10.6 -> 10.2 us and the
     // residual epilogue 16.1 -> 15.5 us at [4096, 1536]; at decode batches
     // (256 rows) the extra round trip before the later chunks costs more
-    // (30.2 -> 30.8 us per C5 layer).  ATLAS_NORM_STAGE (0, 1) overrides.
-    static const int forced_stage = env_int("ATLAS_NORM_STAGE", -1);
-    const bool stage = forced_stage >= 0 ? forced_stage != 0 : a.rows >= 2048;
+    // (30.2 -> 30.8 us per C5 layer).
+    const bool stage = a.rows >= 2048;
     const bool run = par && J > 1 && R == 1 && norm_run(a.rows);
     const size_t lds = run ? (64u * J + 1) * sizeof(f32x4) + sizeof(FoldScansLds<4>)
                            : static_cast<size_t>(R) * (a.hidden / 4 + 1) * sizeof(f32x4);
     const dim3 grid((a.rows + R - 1) / R);
     if constexpr (R == 1 && J > 1) {
         if (run) {
-            if (stage)
-                hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, true, true>), grid, dim3(2 * kWave), lds, s, a);
-            else
-                hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, true>), grid, dim3(2 * kWave), lds, s, a);
+            hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, true>), grid, dim3(2 * kWave), lds, s, a);
             return hipGetLastError();
         }
     }
@@ -538,24 +615,51 @@ template <int MODE>
 hipError_t launch_reg(hipStream_t s, const NormArgs& a) {
     const int J = static_cast<int>((a.hidden / 4 + 63) / 64);
     const RegConfig c = pick_reg(a.rows, MODE);
-    switch (c.rows) {
-        case 4: return launch_reg_r<4, MODE>(s, a, J, c.par);
-        case 2: return launch_reg_r<2, MODE>(s, a, J, c.par);
-        default: return launch_reg_r<1, MODE>(s, a, J, c.par);
+    if (c.rows == 2) return launch_reg_r<2, MODE>(s, a, J, c.par);
+    return launch_reg_r<1, MODE>(s, a, J, c.par);
+}
+
+// Tree engine: two rows per wavefront (rows w and w + G) from 4096 rows up,
+// one row per wavefront below that (fewer rows leave too few wavefronts to
+// fill the chip when each takes two).
+bool tree_pairs(uint32_t rows) { return rows >= 4096; }
+
+template <int J, int MODE>
+hipError_t launch_tree_j(hipStream_t s, const NormArgs& a) {
+    const bool pair = tree_pairs(a.rows);
+    const uint32_t waves = pair ? (a.rows + 1) / 2 : a.rows;
+    const dim3 grid((waves + 3) / 4);
+    if (pair)
+        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, true>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, false>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int MODE>
+hipError_t launch_tree(hipStream_t s, const NormArgs& a) {
+    switch ((a.hidden / 4 + 63) / 64) {
+        case 1: return launch_tree_j<1, MODE>(s, a);
+        case 2: return launch_tree_j<2, MODE>(s, a);
+        case 3: return launch_tree_j<3, MODE>(s, a);
+        case 4: return launch_tree_j<4, MODE>(s, a);
+        case 5: return launch_tree_j<5, MODE>(s, a);
+        case 6: return launch_tree_j<6, MODE>(s, a);
+        case 7: return launch_tree_j<7, MODE>(s, a);
+        default: return launch_tree_j<8, MODE>(s, a);
     }
 }
 
-// Rows per wavefront for the sequential engine: enough wavefronts to keep
-// every SIMD streaming (>= 2048 for large row counts), bounded by 64 KB LDS.
+// Rows per wavefront for the sequential LDS engine: enough wavefronts to
+// keep every SIMD streaming (>= 2048 for large row counts), bounded by 64 KB
+// of LDS.
 int pick_rows(uint32_t rows, uint32_t hidden) {
-    static const int forced = env_int("ATLAS_SEQ_ROWS", 0);
     int best = 1;
     for (int r : {2, 4, 8, 16}) {
         size_t lds = (static_cast<size_t>(r) * (hidden + 4) + r) * 4;
         if (lds > 65536) break;
         if ((rows + r - 1) / r >= 2048) best = r;
     }
-    if (forced > 0) best = forced;
     return best;
 }
 
@@ -743,7 +847,89 @@ __device__ __forceinline__ uint32_t pack16(float lo, float hi) {
     return static_cast<uint32_t>(f2h(lo)) | (static_cast<uint32_t>(f2h(hi)) << 16);
 }
 
-template <int R, int J, bool ADD, bool PAR, bool STAGE>
+// FP16 tree engine (ATLAS_REDUCTION_AUTO and _WIDE): rms_tree_kernel's
+// structure over binary16 rows, one 16-byte access carrying 8 halves.  The
+// math is f32: exact widening, the tree sum of squares, one RNE rounding per
+// output; with a residual, residual_out = rne16(x + r) is stored and the
+// norm reads that rounded value (as the reference's two-kernel chain over
+// f16 buffers does).  y is within one f16 ulp of the sequential fold's.
+template <int J, bool ADD>
+struct TreeRowF16 {
+    u32x4 x[J];
+    u32x4 e[ADD ? J : 1];
+
+    __device__ __forceinline__ void load(const uint16_t* xs, const uint16_t* residual, uint32_t row, uint32_t hidden,
+                                         uint32_t lane, uint32_t n8) {
+        const size_t base = static_cast<size_t>(row) * hidden;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t c = min(lane + 64u * j, n8 - 1);
+            x[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xs + base + 8 * c));
+            if (ADD) e[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(residual + base + 8 * c));
+        }
+    }
+
+    __device__ __forceinline__ void finish(const u32x4 (&w)[J], uint16_t* residual_out, uint16_t* out, uint32_t row,
+                                           uint32_t hidden, uint32_t lane, uint32_t n8, float epsilon) {
+        const size_t base = static_cast<size_t>(row) * hidden;
+        if (ADD) {
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const u32x4 v = x[j], b = e[j];
+                x[j] = u32x4{pack16(lo16(v.x) + lo16(b.x), hi16(v.x) + hi16(b.x)),
+                             pack16(lo16(v.y) + lo16(b.y), hi16(v.y) + hi16(b.y)),
+                             pack16(lo16(v.z) + lo16(b.z), hi16(v.z) + hi16(b.z)),
+                             pack16(lo16(v.w) + lo16(b.w), hi16(v.w) + hi16(b.w))};
+            }
+        }
+        float p = 0.0f;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const u32x4 v = x[j];
+            const float a0 = lo16(v.x), a1 = hi16(v.x), a2 = lo16(v.y), a3 = hi16(v.y);
+            const float a4 = lo16(v.z), a5 = hi16(v.z), a6 = lo16(v.w), a7 = hi16(v.w);
+            const float q = ((a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3)) + ((a4 * a4 + a5 * a5) + (a6 * a6 + a7 * a7));
+            p = p + (lane + 64u * j < n8 ? q : 0.0f);
+        }
+        const float ir = inverse_rms(wave_sum_tree_f32(p), static_cast<float>(hidden), epsilon);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const uint32_t c = lane + 64u * j;
+            if (c >= n8) continue;
+            const u32x4 v = x[j], ww = w[j];
+            if (ADD) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(residual_out + base + 8 * c));
+            const u32x4 y{pack16(lo16(v.x) * ir * lo16(ww.x), hi16(v.x) * ir * hi16(ww.x)),
+                          pack16(lo16(v.y) * ir * lo16(ww.y), hi16(v.y) * ir * hi16(ww.y)),
+                          pack16(lo16(v.z) * ir * lo16(ww.z), hi16(v.z) * ir * hi16(ww.z)),
+                          pack16(lo16(v.w) * ir * lo16(ww.w), hi16(v.w) * ir * hi16(ww.w))};
+            __builtin_nontemporal_store(y, reinterpret_cast<u32x4*>(out + base + 8 * c));
+        }
+    }
+};
+
+template <int J, bool ADD, bool PAIR>
+__global__ __launch_bounds__(256) void rms_tree_f16_kernel(const uint16_t* x, const uint16_t* residual,
+                                                           const uint16_t* weight, uint16_t* residual_out,
+                                                           uint16_t* out, uint32_t rows, uint32_t hidden,
+                                                           float epsilon) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+    const uint32_t r0 = blockIdx.x * 4 + wave;
+    if (r0 >= rows) return;  // wavefront-uniform
+    const uint32_t r1 = r0 + gridDim.x * 4;
+    const bool second = PAIR && r1 < rows;
+    const uint32_t n8 = hidden >> 3;
+    TreeRowF16<J, ADD> row0, row1;
+    row0.load(x, residual, r0, hidden, lane, n8);
+    if (second) row1.load(x, residual, r1, hidden, lane, n8);
+    u32x4 w[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) w[j] = *reinterpret_cast<const u32x4*>(weight + 8 * min(lane + 64u * j, n8 - 1));
+    row0.finish(w, residual_out, out, r0, hidden, lane, n8, epsilon);
+    if (second) row1.finish(w, residual_out, out, r1, hidden, lane, n8, epsilon);
+}
+
+template <int R, int J, bool ADD, bool STAGE>
 __global__ __launch_bounds__(64) void rms_reg_f16_kernel(const uint16_t* x, const uint16_t* residual,
                                                          const uint16_t* weight, uint16_t* residual_out,
                                                          uint16_t* out, uint32_t rows, uint32_t hidden,
@@ -782,7 +968,6 @@ __global__ __launch_bounds__(64) void rms_reg_f16_kernel(const uint16_t* x, cons
     }
 
     float s = 0.0f;
-    uint32_t sb[R];  // PAR: running sums of squares (bit patterns, wave-uniform)
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const uint32_t creal = lane + 64u * j;
@@ -800,41 +985,14 @@ __global__ __launch_bounds__(64) void rms_reg_f16_kernel(const uint16_t* x, cons
             }
             const float a0 = lo16(v.x), a1 = hi16(v.x), a2 = lo16(v.y), a3 = hi16(v.y);
             const float a4 = lo16(v.z), a5 = hi16(v.z), a6 = lo16(v.w), a7 = hi16(v.w);
-            if (!PAR || j == 0) {
-                sq4[r * stride4 + 2 * c] = f32x4{a0 * a0, a1 * a1, a2 * a2, a3 * a3};
-                sq4[r * stride4 + 2 * c + 1] = f32x4{a4 * a4, a5 * a5, a6 * a6, a7 * a7};
-            } else if (static_cast<uint32_t>(r) < nrows) {
-                const bool in_row = creal < n8;
-                const float sq[8] = {in_row ? a0 * a0 : 0.0f, in_row ? a1 * a1 : 0.0f, in_row ? a2 * a2 : 0.0f,
-                                     in_row ? a3 * a3 : 0.0f, in_row ? a4 * a4 : 0.0f, in_row ? a5 * a5 : 0.0f,
-                                     in_row ? a6 * a6 : 0.0f, in_row ? a7 * a7 : 0.0f};
-                sb[r] = fold_chunk_exact<8>(sq, sb[r]);
-            }
+            sq4[r * stride4 + 2 * c] = f32x4{a0 * a0, a1 * a1, a2 * a2, a3 * a3};
+            sq4[r * stride4 + 2 * c + 1] = f32x4{a4 * a4, a5 * a5, a6 * a6, a7 * a7};
         }
-        if (!PAR || j == 0) {
-            __syncthreads();
-            if (lane < nrows) {
-                // PAR: only the first 256 values (lanes 0-31 of chunk 0) fold in order
-                const uint32_t begin = 128u * j, end = min(2 * n8, PAR ? 64u : 128u * (j + 1));
-                const f32x4* row = sq4 + lane * stride4;
-                for (uint32_t k = begin; k < end; k += 64) s = fold_lds_chunk(row + k, min(64u, end - k), s);
-            }
-        }
-        if (PAR && j == 0) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                sb[r] = readlane_u32(__float_as_uint(s), static_cast<uint32_t>(r));
-                if (static_cast<uint32_t>(r) < nrows) {
-                    const u32x4 v = xv[r][0];
-                    const bool take = creal >= 32 && creal < n8;
-                    const float a0 = lo16(v.x), a1 = hi16(v.x), a2 = lo16(v.y), a3 = hi16(v.y);
-                    const float a4 = lo16(v.z), a5 = hi16(v.z), a6 = lo16(v.w), a7 = hi16(v.w);
-                    const float sq[8] = {take ? a0 * a0 : 0.0f, take ? a1 * a1 : 0.0f, take ? a2 * a2 : 0.0f,
-                                         take ? a3 * a3 : 0.0f, take ? a4 * a4 : 0.0f, take ? a5 * a5 : 0.0f,
-                                         take ? a6 * a6 : 0.0f, take ? a7 * a7 : 0.0f};
-                    sb[r] = fold_chunk_exact<8>(sq, sb[r]);
-                }
-            }
+        __syncthreads();
+        if (lane < nrows) {
+            const uint32_t begin = 128u * j, end = min(2 * n8, 128u * (j + 1));
+            const f32x4* row = sq4 + lane * stride4;
+            for (uint32_t k = begin; k < end; k += 64) s = fold_lds_chunk(row + k, min(64u, end - k), s);
         }
     }
     if (ADD) {
@@ -854,8 +1012,7 @@ __global__ __launch_bounds__(64) void rms_reg_f16_kernel(const uint16_t* x, cons
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         if (static_cast<uint32_t>(r) >= nrows) break;
-        const float ir = PAR ? inverse_rms(__uint_as_float(sb[r]), static_cast<float>(hidden), epsilon)
-                             : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
+        const float ir = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const uint32_t c = lane + 64u * j;
@@ -870,71 +1027,93 @@ __global__ __launch_bounds__(64) void rms_reg_f16_kernel(const uint16_t* x, cons
     }
 }
 
-template <int R, int J, bool ADD>
-hipError_t launch_f16_reg_rj(hipStream_t s, const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
-                             uint16_t* residual_out, uint16_t* out, uint32_t rows, uint32_t hidden, float eps) {
-    const size_t lds = static_cast<size_t>(R) * (hidden / 4 + 1) * sizeof(f32x4);
-    // FP16 rows ([2048, 2048] at C2) measured slower with the parallel fold
-    // (13.8 -> 16.7 us), so the in-order fold is the default here;
-    // ATLAS_NORM_PAR_FOLD=1 selects the parallel one (same bits).
-    static const int forced_stage = env_int("ATLAS_NORM_STAGE", -1);
-    const bool stage = forced_stage >= 0 ? forced_stage != 0 : rows >= 2048;
-    const dim3 grid((rows + R - 1) / R);
-    if (env_int("ATLAS_NORM_PAR_FOLD", 0) == 1)
-        hipLaunchKernelGGL((rms_reg_f16_kernel<R, J, ADD, true, false>), grid, dim3(kWave), lds, s, x, residual,
-                           weight, residual_out, out, rows, hidden, eps);
-    else if (stage)
-        hipLaunchKernelGGL((rms_reg_f16_kernel<R, J, ADD, false, true>), grid, dim3(kWave), lds, s, x, residual,
-                           weight, residual_out, out, rows, hidden, eps);
+template <int J, bool ADD>
+hipError_t launch_f16_reg_j(hipStream_t s, const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
+                            uint16_t* residual_out, uint16_t* out, uint32_t rows, uint32_t hidden, float eps) {
+    // one row per wavefront (C2 [2048, 2048]: 13.2 us, against 13.6 with two
+    // rows per wavefront), staged loads from 2048 rows up; the exact
+    // wave-parallel fold measured slower here (13.8 -> 16.7 us), so every
+    // chunk folds in order
+    const size_t lds = (hidden / 4 + 1) * sizeof(f32x4);
+    const dim3 grid(rows);
+    if (rows >= 2048)
+        hipLaunchKernelGGL((rms_reg_f16_kernel<1, J, ADD, true>), grid, dim3(kWave), lds, s, x, residual, weight,
+                           residual_out, out, rows, hidden, eps);
     else
-        hipLaunchKernelGGL((rms_reg_f16_kernel<R, J, ADD, false, false>), grid, dim3(kWave), lds, s, x, residual,
-                           weight, residual_out, out, rows, hidden, eps);
+        hipLaunchKernelGGL((rms_reg_f16_kernel<1, J, ADD, false>), grid, dim3(kWave), lds, s, x, residual, weight,
+                           residual_out, out, rows, hidden, eps);
     return hipGetLastError();
 }
 
-template <int R, bool ADD>
-hipError_t launch_f16_reg_r(hipStream_t s, int J, const uint16_t* x, const uint16_t* residual,
-                            const uint16_t* weight, uint16_t* residual_out, uint16_t* out, uint32_t rows,
-                            uint32_t hidden, float eps) {
-    switch (J) {
-        case 1: return launch_f16_reg_rj<R, 1, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
-        case 2: return launch_f16_reg_rj<R, 2, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
-        case 3: return launch_f16_reg_rj<R, 3, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
-        case 4: return launch_f16_reg_rj<R, 4, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
-        case 5: return launch_f16_reg_rj<R, 5, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
-        case 6: return launch_f16_reg_rj<R, 6, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
-        case 7: return launch_f16_reg_rj<R, 7, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
-        default: return launch_f16_reg_rj<R, 8, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
-    }
+template <int J, bool ADD>
+hipError_t launch_f16_tree_j(hipStream_t s, const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
+                             uint16_t* residual_out, uint16_t* out, uint32_t rows, uint32_t hidden, float eps) {
+    const bool pair = tree_pairs(rows);
+    const uint32_t waves = pair ? (rows + 1) / 2 : rows;
+    const dim3 grid((waves + 3) / 4);
+    if (pair)
+        hipLaunchKernelGGL((rms_tree_f16_kernel<J, ADD, true>), grid, dim3(256), 0, s, x, residual, weight,
+                           residual_out, out, rows, hidden, eps);
+    else
+        hipLaunchKernelGGL((rms_tree_f16_kernel<J, ADD, false>), grid, dim3(256), 0, s, x, residual, weight,
+                           residual_out, out, rows, hidden, eps);
+    return hipGetLastError();
 }
 
+// hidden % 8 == 0, hidden <= 4096 (J <= 8 chunks of 512 halves)
 template <bool ADD>
-hipError_t launch_f16_reg(hipStream_t s, const uint16_t* x, const uint16_t* residual, const uint16_t* weight,
-                          uint16_t* residual_out, uint16_t* out, uint32_t rows, uint32_t hidden, float eps) {
-    const int J = static_cast<int>((hidden / 8 + 63) / 64);
-    // one row per wavefront with staged loads from 2048 rows up (C2
-    // [2048, 2048]: 13.2 us, against 13.6 with two rows per wavefront);
-    // ATLAS_REG_ROWS (1, 2) overrides for sweeps
-    const int forced = env_int("ATLAS_REG_ROWS", 0);
-    if (forced == 2)
-        return launch_f16_reg_r<2, ADD>(s, J, x, residual, weight, residual_out, out, rows, hidden, eps);
-    return launch_f16_reg_r<1, ADD>(s, J, x, residual, weight, residual_out, out, rows, hidden, eps);
+hipError_t launch_f16_vec(hipStream_t s, bool tree, const uint16_t* x, const uint16_t* residual,
+                          const uint16_t* weight, uint16_t* residual_out, uint16_t* out, uint32_t rows,
+                          uint32_t hidden, float eps) {
+#define ATLAS_F16_J(JJ)                                                                                        \
+    case JJ:                                                                                                    \
+        return tree ? launch_f16_tree_j<JJ, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps) \
+                    : launch_f16_reg_j<JJ, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
+    switch ((hidden / 8 + 63) / 64) {
+        ATLAS_F16_J(1)
+        ATLAS_F16_J(2)
+        ATLAS_F16_J(3)
+        ATLAS_F16_J(4)
+        ATLAS_F16_J(5)
+        ATLAS_F16_J(6)
+        ATLAS_F16_J(7)
+        default:
+            return tree ? launch_f16_tree_j<8, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps)
+                        : launch_f16_reg_j<8, ADD>(s, x, residual, weight, residual_out, out, rows, hidden, eps);
+    }
+#undef ATLAS_F16_J
 }
 
 }  // namespace
 
+// Engine choice.  kSequential: the sequential fold everywhere (register
+// engine, or the LDS engine for hidden > 2048 or unaligned rows).  kAuto
+// (the default): the tree engine where the output is a plain scaled row
+// (RMSNorm, the add-norm's y), the sequential fold where an epilogue
+// cancels (residual add, PLE add-scale), whose elementwise error would
+// otherwise be unbounded relative to the output.  kWide: the tree engine
+// everywhere.
 hipError_t launch_rms_norm_f32(hipStream_t stream, NormMode mode, Reduction red, const NormArgs& a) {
-    bool vec = (a.hidden % 4) == 0 && aligned16(a.x) && aligned16(a.weight) && aligned16(a.out) &&
-               (!a.residual || aligned16(a.residual)) && (!a.normalized || aligned16(a.normalized)) &&
-               (!a.residual_out || aligned16(a.residual_out));
-    if (red == kWide) {
+    const bool vec = (a.hidden % 4) == 0 && aligned16(a.x) && aligned16(a.weight) && aligned16(a.out) &&
+                     (!a.residual || aligned16(a.residual)) && (!a.normalized || aligned16(a.normalized)) &&
+                     (!a.residual_out || aligned16(a.residual_out));
+    const bool cancels = mode == kNormResidual || mode == kNormAddScale;
+    const bool tree = red == kWide || (red == kAuto && !cancels);
+    if (tree && vec && a.hidden <= 2048) {
+        switch (mode) {
+            case kNormPlain: return launch_tree<kNormPlain>(stream, a);
+            case kNormResidual: return launch_tree<kNormResidual>(stream, a);
+            case kNormAddNorm: return launch_tree<kNormAddNorm>(stream, a);
+            case kNormAddScale: return launch_tree<kNormAddScale>(stream, a);
+        }
+    } else if (tree) {
         switch (mode) {
             case kNormPlain: return launch_wide<kNormPlain>(stream, a, vec);
             case kNormResidual: return launch_wide<kNormResidual>(stream, a, vec);
             case kNormAddNorm: return launch_wide<kNormAddNorm>(stream, a, vec);
             case kNormAddScale: return launch_wide<kNormAddScale>(stream, a, vec);
         }
-    } else if (vec && a.hidden <= 2048 && !lds_engine_forced()) {
+    } else if (vec && a.hidden <= 2048) {
         switch (mode) {
             case kNormPlain: return launch_reg<kNormPlain>(stream, a);
             case kNormResidual: return launch_reg<kNormResidual>(stream, a);
@@ -955,25 +1134,30 @@ hipError_t launch_rms_norm_f32(hipStream_t stream, NormMode mode, Reduction red,
 hipError_t launch_rms_norm_groups_stable_f32(hipStream_t stream, Reduction red, float* values,
                                              const float* weight, uint32_t width, uint32_t groups,
                                              float epsilon) {
-    const size_t lds = red == kSequential ? static_cast<size_t>(width) * sizeof(float) : 0;
+    // kAuto keeps the sequential fold: one wavefront per 256-wide group folds
+    // its squares in order from LDS at no measurable cost
+    const bool seq = red != kWide;
+    const size_t lds = seq ? static_cast<size_t>(width) * sizeof(float) : 0;
     hipLaunchKernelGGL(groups_stable_kernel, dim3(groups), dim3(kWave), lds, stream, values, weight,
-                       width, groups, epsilon, red == kSequential ? 1 : 0);
+                       width, groups, epsilon, seq ? 1 : 0);
     return hipGetLastError();
 }
 
+// FP16 rows: the outputs are plain scaled rows (residual_out does not
+// depend on the reduction), so kAuto and kWide take the tree engine.
 hipError_t launch_rms_norm_f16(hipStream_t stream, Reduction red, const uint16_t* x,
                                const uint16_t* residual, const uint16_t* weight,
                                uint16_t* residual_out, uint16_t* out, uint32_t rows,
                                uint32_t hidden, float epsilon) {
-    const int seq = red == kSequential ? 1 : 0;
-    const bool reg = seq && hidden % 8 == 0 && hidden <= 4096 && aligned16(x) && aligned16(weight) &&
-                     aligned16(out) && (!residual || (aligned16(residual) && aligned16(residual_out))) &&
-                     !lds_engine_forced();
-    if (reg) {
+    const bool tree = red != kSequential;
+    const bool vec = hidden % 8 == 0 && hidden <= 4096 && aligned16(x) && aligned16(weight) && aligned16(out) &&
+                     (!residual || (aligned16(residual) && aligned16(residual_out)));
+    if (vec) {
         if (residual)
-            return launch_f16_reg<true>(stream, x, residual, weight, residual_out, out, rows, hidden, epsilon);
-        return launch_f16_reg<false>(stream, x, residual, weight, residual_out, out, rows, hidden, epsilon);
+            return launch_f16_vec<true>(stream, tree, x, residual, weight, residual_out, out, rows, hidden, epsilon);
+        return launch_f16_vec<false>(stream, tree, x, residual, weight, residual_out, out, rows, hidden, epsilon);
     }
+    const int seq = tree ? 0 : 1;
     const size_t lds = seq ? static_cast<size_t>(hidden) * sizeof(float) : 0;
     if (residual)
         hipLaunchKernelGGL((rms_f16_seq_kernel<true>), dim3(rows), dim3(kWave), lds, stream, x,

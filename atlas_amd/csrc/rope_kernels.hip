@@ -22,7 +22,6 @@
 #include "device_common.hpp"
 #include "launch.hpp"
 
-#include <stdlib.h>
 
 namespace atlas {
 namespace {
@@ -516,14 +515,6 @@ __global__ __launch_bounds__(256) void rope_interleaved_kernel(const float* x, c
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
-bool qk_legacy_forced() {
-    static const bool forced = [] {
-        const char* v = getenv("ATLAS_QK_UNIT_ENGINE");
-        return v && *v && atoi(v) != 0;
-    }();
-    return forced;
-}
-
 template <int V, int UNITS>
 hipError_t launch_qk(hipStream_t s, bool seq, const float* q, const float* k, const float* qw,
                      const float* kw, const float* c, const float* sn, float* qo, float* ko,
@@ -548,7 +539,9 @@ hipError_t launch_qk_norm_rope_f32(hipStream_t stream, Reduction red, const floa
                                    float* k_out, uint32_t tokens, uint32_t q_heads,
                                    uint32_t has_key, uint32_t head_dim, uint32_t rope_stride,
                                    float epsilon) {
-    const bool seq = red == kSequential;
+    // the rotation after the norm can cancel, so only ATLAS_REDUCTION_WIDE
+    // reorders the sum of squares here; kAuto keeps the sequential fold
+    const bool seq = red != kWide;
     // Token engine: head_dim = 128*P, at most 16 units per token, operands
     // and per-token cos/sin rows aligned to P floats.
     {
@@ -557,8 +550,7 @@ hipError_t launch_qk_norm_rope_f32(hipStream_t stream, Reduction red, const floa
         const bool ok = seq && head_dim % 128 == 0 && (P == 1 || P == 2 || P == 4) && q_heads + has_key <= 16 &&
                         q_heads + has_key > 0 && aligned(q, pa) && aligned(q_out, pa) && aligned(q_weight, pa) &&
                         aligned(cosine, pa) && aligned(sine, pa) && rope_stride % P == 0 &&
-                        (!has_key || (aligned(k, pa) && aligned(k_out, pa) && aligned(k_weight, pa))) &&
-                        !qk_legacy_forced();
+                        (!has_key || (aligned(k, pa) && aligned(k_out, pa) && aligned(k_weight, pa)));
         if (ok) {
             if (P == 1)
                 return launch_qk_token_p<1>(stream, q, k, q_weight, k_weight, cosine, sine, q_out, k_out, tokens,
@@ -759,19 +751,11 @@ bool launch_rope_half_token(hipStream_t stream, const void* x0, void* out0, uint
 #undef ATLAS_ROPE_TOKEN_CASE
 }
 
-bool rope_token_disabled() {
-    static const bool off = [] {
-        const char* v = getenv("ATLAS_ROPE_TOKEN");
-        return v && *v == '0';
-    }();
-    return off;
-}
-
 hipError_t launch_rope_half_pair_f32(hipStream_t stream, const float* x0, float* out0, uint32_t heads0,
                                      const float* x1, float* out1, uint32_t heads1, const float* cosine,
                                      const float* sine, uint32_t tokens, uint32_t head_dim, uint32_t rope_stride) {
-    if (!rope_token_disabled() && launch_rope_half_token<false>(stream, x0, out0, heads0, x1, out1, heads1, cosine,
-                                                                sine, tokens, head_dim, rope_stride))
+    if (launch_rope_half_token<false>(stream, x0, out0, heads0, x1, out1, heads1, cosine, sine, tokens, head_dim,
+                                      rope_stride))
         return hipGetLastError();
     const uint32_t half = head_dim / 2;
     const bool vec = (half % 4) == 0 && (rope_stride % 4) == 0 && aligned(x0, 16) && aligned(out0, 16) &&
@@ -792,8 +776,8 @@ hipError_t launch_rope_half_pair_f32(hipStream_t stream, const float* x0, float*
 hipError_t launch_rope_half_pair_f16(hipStream_t stream, const uint16_t* x0, uint16_t* out0, uint32_t heads0,
                                      const uint16_t* x1, uint16_t* out1, uint32_t heads1, const float* cosine,
                                      const float* sine, uint32_t tokens, uint32_t head_dim, uint32_t rope_stride) {
-    if (!rope_token_disabled() && launch_rope_half_token<true>(stream, x0, out0, heads0, x1, out1, heads1, cosine,
-                                                               sine, tokens, head_dim, rope_stride))
+    if (launch_rope_half_token<true>(stream, x0, out0, heads0, x1, out1, heads1, cosine, sine, tokens, head_dim,
+                                     rope_stride))
         return hipGetLastError();
     const uint32_t half = head_dim / 2;
     const bool vec = (half % 8) == 0 && (rope_stride % 4) == 0 && aligned(x0, 16) && aligned(out0, 16) &&

@@ -82,7 +82,7 @@ class DeviceBuffer:
 class HipRuntime:
     """Device context: MetalRuntime::new (crates/atlas-metal/src/lib.rs:909-1061)."""
 
-    def __init__(self, device: int = 0, reduction: int = _lib.ATLAS_REDUCTION_SEQUENTIAL):
+    def __init__(self, device: int = 0, reduction: int = _lib.ATLAS_REDUCTION_AUTO):
         self.lib = _lib.load()
         ctx = c_void_p()
         rc = self.lib.atlas_hip_init(device, byref(ctx))

@@ -25,7 +25,7 @@ floor of launch plus memory system -- and `of_floor` = floor_us / us.
 The CPU baseline is the oracle (a single-threaded C restatement of the
 reference CPU operators) timed on this host over a bounded token sample.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--reduction sequential|wide]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--reduction auto|sequential|wide]
        python bench.py --only geglu,rms_norm        (per-op timing only, for profiling)
        python bench.py --copy-mib 256               (a D2D copy of known size: the PMC
                                                       calibration kernel)
@@ -276,14 +276,17 @@ def time_launches(rt, launch, sets, iters):
 
 
 class StreamFloor:
-    """Size-matched streaming floor for an op: one launch of a plain streaming
-    kernel (atlas_amd/libatlas_stream_floor.so, measurement only) that reads
-    the op's input bytes and writes its output bytes as contiguous 128-bit
-    nontemporal streams, with one and with four float4 per thread; the floor
-    is the faster of the two.  Timed like the ops: HIP events on the library's
-    stream around back-to-back launches, rotating over >= 1 GiB of distinct
-    buffers.  What the launch path and the memory system give for that many
-    bytes at that size, with no arithmetic, reduction or gather."""
+    """Size-matched streaming floor for an op: plain streaming kernels
+    (atlas_amd/libatlas_stream_floor.so, measurement only) that read the op's
+    input bytes and write its output bytes as contiguous 128-bit streams, in
+    three shapes (one float4 per thread with nontemporal loads and stores; a
+    4096-workgroup grid striding over the streams with sc1+nt stores; one
+    float4 per thread with plain loads), the fastest of a sweep over cache
+    policies and grid shapes; the floor is the fastest of the three.  Timed
+    like the ops: HIP events on the library's stream around back-to-back
+    launches, rotating over >= 1 GiB of distinct buffers.  What the launch
+    path and the memory system give for that many bytes at that size, with no
+    arithmetic, reduction or gather."""
 
     def __init__(self, rt):
         import ctypes
@@ -292,9 +295,10 @@ class StreamFloor:
         if not os.path.exists(path):
             raise RuntimeError(f"{path} is not built (run __graft_entry__.build())")
         self.lib = ctypes.CDLL(path)
-        self.lib.atlas_floor_stream_per.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
-                                                    ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int]
-        self.lib.atlas_floor_stream_per.restype = ctypes.c_int
+        self.lib.atlas_floor_stream_kind.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                                     ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int]
+        self.lib.atlas_floor_stream_kind.restype = ctypes.c_int
+        self.lib.atlas_floor_kinds.restype = ctypes.c_int
         self.lib.atlas_floor_launch.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p]
         self.lib.atlas_floor_launch.restype = ctypes.c_int
         self.rt = rt
@@ -302,34 +306,37 @@ class StreamFloor:
         self.sink = rt.alloc(256)
 
     def us(self, in_bytes, out_bytes, iters):
-        return min(self.us_per(in_bytes, out_bytes, iters, per) for per in (1, 4))
+        return min(self.us_kinds(in_bytes, out_bytes, iters).values())
 
-    def us_per(self, in_bytes, out_bytes, iters, per):
+    def us_kinds(self, in_bytes, out_bytes, iters):
+        """Microseconds per launch of every shape, {kind: us}, on one pool."""
         rt = self.rt
         ib, ob = (in_bytes + 255) // 256 * 256, (out_bytes + 255) // 256 * 256
         per_set = ib + ob
         nsets = max(4, math.ceil(ROTATION_BYTES / per_set))
         pool = rt.alloc(nsets * per_set)
         rt.memset(pool, 0, nsets * per_set)
+        result = {}
+        for kind in range(self.lib.atlas_floor_kinds()):
+            def launch(i):
+                base = pool.ptr + (i % nsets) * per_set
+                rc = self.lib.atlas_floor_stream_kind(self.stream, base, in_bytes, base + ib, out_bytes,
+                                                      self.sink.ptr, kind)
+                if rc != 0:
+                    raise RuntimeError(f"stream floor launch failed: HIP error {rc}")
 
-        def launch(i):
-            base = pool.ptr + (i % nsets) * per_set
-            rc = self.lib.atlas_floor_stream_per(self.stream, base, in_bytes, base + ib, out_bytes, self.sink.ptr, per)
-            if rc != 0:
-                raise RuntimeError(f"stream floor launch failed: HIP error {rc}")
-
-        for i in range(3):
-            launch(i)
-        rt.sync()
-        a, b = rt.event(), rt.event()
-        rt.record(a)
-        for i in range(iters):
-            launch(i)
-        rt.record(b)
-        rt.sync()
-        us = rt.elapsed_ms(a, b) / iters * 1e3
+            for i in range(3):
+                launch(i)
+            rt.sync()
+            a, b = rt.event(), rt.event()
+            rt.record(a)
+            for i in range(iters):
+                launch(i)
+            rt.record(b)
+            rt.sync()
+            result[kind] = rt.elapsed_ms(a, b) / iters * 1e3
         rt.free(pool)
-        return us
+        return result
 
     def launch_us(self, blocks, iters):
         """Back-to-back launches of `blocks` empty one-wavefront workgroups."""
@@ -370,8 +377,10 @@ def floor_sweep(rt, iters):
              (16.8, 16.8), (42.0, 37.7), (50.3, 25.2), (67.1, 33.6), (201.3, 100.7), (171.1, 143.2)]
     for r_mb, w_mb in sizes:
         ib, ob = int(r_mb * 1e6) // 16 * 16, int(w_mb * 1e6) // 16 * 16
-        us = floor.us(ib, ob, iters)
+        kinds = floor.us_kinds(ib, ob, iters)
+        us = min(kinds.values())
         print(json.dumps({"read_MB": r_mb, "write_MB": w_mb, "us": round(us, 3),
+                          "us_by_kind": {k: round(v, 3) for k, v in kinds.items()},
                           "GB/s": round((ib + ob) / (us * 1e-6) / 1e9, 1),
                           "frac": round((ib + ob) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
 
@@ -518,7 +527,9 @@ def main():
     # the average is taken at steady clocks (100 measured 1-2 % slower)
     ap.add_argument("--op-iters", type=int, default=1000)
     ap.add_argument("--step-sets", type=int, default=4)
-    ap.add_argument("--reduction", choices=["sequential", "wide"], default="sequential")
+    ap.add_argument("--reduction", choices=["auto", "sequential", "wide"], default="auto",
+                    help="row-sum order: auto (the library default: tree where the output is a plain scaled row, "
+                         "sequential where an epilogue cancels), sequential (bit-identical everywhere), wide")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-floor", action="store_true",
@@ -540,10 +551,12 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    from atlas_amd import ATLAS_REDUCTION_SEQUENTIAL, ATLAS_REDUCTION_WIDE, HipRuntime, rope_tables_gemma4
+    from atlas_amd import (ATLAS_REDUCTION_AUTO, ATLAS_REDUCTION_SEQUENTIAL, ATLAS_REDUCTION_WIDE, HipRuntime,
+                           rope_tables_gemma4)
     from atlas_amd import workloads as wl
 
-    rt = HipRuntime(0, ATLAS_REDUCTION_WIDE if args.reduction == "wide" else ATLAS_REDUCTION_SEQUENTIAL)
+    rt = HipRuntime(0, {"auto": ATLAS_REDUCTION_AUTO, "sequential": ATLAS_REDUCTION_SEQUENTIAL,
+                        "wide": ATLAS_REDUCTION_WIDE}[args.reduction])
     if args.floor_sweep:
         floor_sweep(rt, args.op_iters)
         rt.close()

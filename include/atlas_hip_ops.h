@@ -22,12 +22,19 @@
  *    reference's predicates, copy in, run, copy out, synchronise, and fill an
  *    atlas_dispatch_timing.  Invalid input returns ATLAS_ERR_INVALID_INPUT
  *    before any device work, like MetalError::InvalidInput.
- *  - Reduction order: ATLAS_REDUCTION_SEQUENTIAL (default) folds the per-row
- *    sum of squares left to right in f32, bit-identical to the reference's
- *    CPU operators (crates/atlas-ops/tests/phase_02_operators.rs:223-242).
- *    ATLAS_REDUCTION_WIDE uses lane-parallel partial sums + a cross-lane tree,
- *    the strategy of the reference's rms_norm_decode_batch_f32 and
- *    *_wide kernels (crates/atlas-metal/src/kernels.metal:119-133,1053-1195).
+ *  - Reduction order of the row sums of squares (atlas_hip_set_reduction):
+ *    ATLAS_REDUCTION_SEQUENTIAL folds left to right in f32, bit-identical to
+ *    the reference's CPU operators (crates/atlas-ops/tests/
+ *    phase_02_operators.rs:223-242).  ATLAS_REDUCTION_WIDE uses lane-parallel
+ *    partial sums + a cross-lane tree everywhere, the strategy of the
+ *    reference's rms_norm_decode_batch_f32 and *_wide kernels
+ *    (crates/atlas-metal/src/kernels.metal:119-133,1053-1195).
+ *    ATLAS_REDUCTION_AUTO (the default) takes the tree where the output is a
+ *    plain scaled row (rms_norm f32/f16, the add-norm's y: within 2e-6
+ *    relative of the CPU operator on the configs' rows) and the sequential
+ *    fold where an epilogue can cancel (the residual and add-scale
+ *    epilogues, QK-norm + RoPE, the stable group norm), so those stay
+ *    bit-identical to the CPU operators.
  *  - One context per host thread; calls on one context are not re-entrant.
  */
 #ifndef ATLAS_HIP_OPS_H
@@ -53,7 +60,8 @@ typedef enum atlas_status {
 
 typedef enum atlas_reduction {
     ATLAS_REDUCTION_SEQUENTIAL = 0,
-    ATLAS_REDUCTION_WIDE = 1
+    ATLAS_REDUCTION_WIDE = 1,
+    ATLAS_REDUCTION_AUTO = 2
 } atlas_reduction;
 
 /* DispatchTiming (crates/atlas-metal/src/lib.rs:81-88). */

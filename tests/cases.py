@@ -25,6 +25,32 @@ def digest(arrays) -> str:
     return h.hexdigest()
 
 
+# -------------------------------------------------------------- comparisons
+
+def assert_bits(name, got, exp):
+    assert len(got) == len(exp), name
+    for i, (g, e) in enumerate(zip(got, exp)):
+        g, e = np.asarray(g).reshape(-1), np.asarray(e).reshape(-1)
+        assert g.shape == e.shape, (name, i, g.shape, e.shape)
+        gb, eb = g.view(np.uint8), e.view(np.uint8)
+        if not np.array_equal(gb, eb):
+            gf, ef = g.astype(np.float64), e.astype(np.float64)
+            mism = np.nonzero((g != e) & ~(np.isnan(gf) & np.isnan(ef)))[0]
+            j = mism[0] if mism.size else 0
+            raise AssertionError(f"{name}[{i}]: {mism.size} of {g.size} elements differ; first at {j}: "
+                                 f"gpu={g[j]!r} oracle={e[j]!r} max_abs={np.nanmax(np.abs(gf - ef)):.3e}")
+
+
+def assert_bits_nan_equal(name, got, exp):
+    for i, (g, e) in enumerate(zip(got, exp)):
+        g, e = np.asarray(g).reshape(-1), np.asarray(e).reshape(-1)
+        same = (g.view(np.uint32) == e.view(np.uint32)) | (np.isnan(g) & np.isnan(e))
+        if not same.all():
+            j = int(np.nonzero(~same)[0][0])
+            raise AssertionError(f"{name}[{i}]: {int((~same).sum())} of {g.size} differ; first at {j}: "
+                                 f"gpu={g[j]!r} oracle={e[j]!r}")
+
+
 # ---------------------------------------------------------------- builders
 
 def rms_case(rows, hidden, eps, seed, mode="plain"):
@@ -255,6 +281,74 @@ def swiglu_f16_gpu(rt, inp, m):
     rt.swiglu_f16(g, u, o, m["n"])
     rt.sync()
     return [o.download(m["n"])]
+
+
+# ------------------------------------------------------- adversarial rows
+
+def adversarial_rows(rows, hidden, seed):
+    """Rows that stress the exact wave-parallel fold of the sum of squares:
+    rounding ties, binade crossings, zeros, subnormal and overflowing squares,
+    non-finite values, wide exponent ranges and a sum that grows through many
+    binades."""
+    r = np.random.default_rng(seed)
+    x = r.standard_normal((rows, hidden)).astype(f32)
+    for i in range(rows):
+        kind = i % 16
+        row = x[i]
+        if kind == 1:
+            row *= f32(1e-20)                                   # subnormal squares
+        elif kind == 2:
+            row *= f32(1e18)                                    # sum overflows to inf
+        elif kind == 3:
+            row[r.random(hidden) < 0.5] = 0.0                   # many zeros
+        elif kind == 4:
+            row[:] = np.trunc(row * 4) / 4                      # coarse values: many exact ties
+        elif kind == 5:
+            row[7] = np.inf
+        elif kind == 6:
+            row[hidden // 3] = np.nan
+        elif kind == 7:
+            row[:] = 1.0
+        elif kind == 8:
+            row[:] = (np.arange(hidden) % 7) * f32(0.5)
+        elif kind == 9:
+            row[:100] *= f32(1e-3)                              # slow start
+        elif kind == 10:
+            row[:] = np.ldexp(1.0 + r.random(hidden), r.integers(-20, 20, hidden)).astype(f32)
+        elif kind == 11:
+            row[:] = 0.0
+        elif kind == 12:
+            row[:] = np.sqrt(np.ldexp(1.0, r.integers(0, 8, hidden))).astype(f32)
+        elif kind == 13:
+            row *= f32(1e-6)
+        elif kind == 14:
+            row[:] = np.trunc(row * 64) / 64
+        elif kind == 15:
+            # squares growing geometrically 1 .. 2^16: the sum climbs past the
+            # four binades the decode-batch fold scans ahead, mid-row
+            row[:] = np.sqrt(np.exp2(np.arange(hidden) * (16.0 / hidden))).astype(f32)
+    return x.reshape(-1)
+
+
+def adversarial_f16_rows(rows, hidden, seed):
+    """FP16 rows built to break a reordered or wave-parallel fold: squares of f16
+    values have few significant bits, so exact rounding ties are frequent; plus
+    binade crossings from tiny to large sums, subnormal and zero stretches,
+    mixed magnitudes, and inf / NaN."""
+    r = np.random.default_rng(seed)
+    x = r.standard_normal((rows, hidden)).astype(np.float16)
+    kind = np.arange(rows) % 7
+    few = np.array([0.5, 1.0, 1.5, 2.0, 2.5, 3.0, 0.75, 1.25], np.float16)
+    x[kind == 1] = r.choice(few, (int((kind == 1).sum()), hidden)) * r.choice([-1, 1], (int((kind == 1).sum()), hidden))
+    x[kind == 2] = (r.standard_normal((int((kind == 2).sum()), hidden)) * 1e-6).astype(np.float16)   # subnormal f16
+    big = kind == 3
+    x[big] = (r.standard_normal((int(big.sum()), hidden)) * np.where(r.random((int(big.sum()), hidden)) < 0.1, 3e3, 1e-2)
+              ).astype(np.float16)
+    sparse = kind == 4
+    x[sparse] = np.where(r.random((int(sparse.sum()), hidden)) < 0.05, x[sparse], np.float16(0))
+    x[kind == 5, hidden // 3] = np.float16(np.inf)
+    x[kind == 6, hidden // 2] = np.float16(np.nan)
+    return x.reshape(-1).view(np.uint16)
 
 
 # ------------------------------------------------------------ case registry

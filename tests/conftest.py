@@ -26,9 +26,22 @@ def ora():
 
 @pytest.fixture(scope="session")
 def rt():
-    """One HIP context for the whole GPU session (fails loudly when absent)."""
-    from atlas_amd import HipRuntime
+    """One HIP context for the bit-exact parity tests: the sequential
+    reduction, so every op reproduces the CPU operators' bits (fails loudly
+    when no GPU or library is present)."""
+    from atlas_amd import ATLAS_REDUCTION_SEQUENTIAL, HipRuntime
 
-    runtime = HipRuntime(0)
+    runtime = HipRuntime(0, ATLAS_REDUCTION_SEQUENTIAL)
+    yield runtime
+    runtime.close()
+
+
+@pytest.fixture(scope="session")
+def rt_auto():
+    """A context with the library's default reduction (ATLAS_REDUCTION_AUTO):
+    the tree engines for plain scaled rows, the sequential fold elsewhere."""
+    from atlas_amd import ATLAS_REDUCTION_AUTO, HipRuntime
+
+    runtime = HipRuntime(0, ATLAS_REDUCTION_AUTO)
     yield runtime
     runtime.close()

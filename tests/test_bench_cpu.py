@@ -22,10 +22,11 @@ def test_cpu_baseline_fields_single_and_threaded():
 
 def test_stream_floor_library_exports():
     """The measurement-only floor library bench.py loads: built, loadable
-    without a GPU, and exporting the three entry points bench.py binds."""
+    without a GPU, and exporting the entry points bench.py binds."""
     import ctypes
     path = os.path.join(ROOT, "atlas_amd", "libatlas_stream_floor.so")
     assert os.path.exists(path), "run __graft_entry__.build() first"
     lib = ctypes.CDLL(path)
-    for name in ("atlas_floor_stream", "atlas_floor_stream_per", "atlas_floor_launch"):
+    for name in ("atlas_floor_stream_kind", "atlas_floor_kinds", "atlas_floor_launch"):
         assert hasattr(lib, name), name
+    assert lib.atlas_floor_kinds() == 3

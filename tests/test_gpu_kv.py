@@ -2,7 +2,7 @@
 with and without the fused V RMSNorm) through the C ABI.  The whole cache is
 compared byte for byte with the CPU restatement of the Metal kernels.  Widths
 256, 512 and 1024 run the row engine (two wavefronts per token); the others
-run the per-value engine (ATLAS_KV_ROW=0 forces it for every width)."""
+run the per-value engine."""
 import sys
 
 import numpy as np
@@ -33,7 +33,13 @@ def run(rt, ora, fmt, key, value, w, cap, pos, vnorm, fill=0x5A):
     return got, exp, dv.download(value.size, np.float32)
 
 
-def assert_cache(name, got, exp):
+def assert_cache(name, got, exp, fmt=None):
+    if fmt == "f32":
+        # f32 caches: a NaN equals any NaN (payload bits are not part of the contract)
+        g, e = got.view(np.float32), exp.view(np.float32)
+        both_nan = np.isnan(g) & np.isnan(e)
+        got = np.where(both_nan, np.float32(0), g).view(np.uint8)
+        exp = np.where(both_nan, np.float32(0), e).view(np.uint8)
     if not np.array_equal(got, exp):
         j = int(np.nonzero(got != exp)[0][0])
         raise AssertionError(f"{name}: {int((got != exp).sum())} of {exp.size} cache bytes differ; first at {j}: "
@@ -63,16 +69,23 @@ def _values(r, tokens, w, kind):
         v[2::5, ::7] = np.float32(1e30)
         v[3::5] = np.where(np.arange(w) % 2 == 0, f32(2.5), f32(-2.5))        # |max| ties, mixed signs
         v[4::5] *= f32(1e-20)                                # subnormal squares in the V norm
+    elif kind == "nan":
+        nan = f32(np.nan)
+        v[0::4, :32] = nan                                   # an all-NaN block: scale 0, codes 0
+        v[1::4, 5] = nan                                     # one NaN: with the V norm the whole row is NaN
+        v[2::4] = nan                                        # an all-NaN row
+        v[3::4, ::3] = nan                                   # NaN beside finite values in every block
     return v
 
 
 @pytest.mark.parametrize("fmt", ["f32", "q8_0", "q4_0"])
 @pytest.mark.parametrize("w,tokens,cap", [(256, 1, 64), (512, 1, 4096), (256, 4096, 4096), (32, 9, 16),
                                           (4096, 3, 4), (96, 33, 40), (1024, 130, 128)])
-@pytest.mark.parametrize("kind", ["normal", "adversarial"])
+@pytest.mark.parametrize("kind", ["normal", "adversarial", "nan"])
 def test_kv_append_shapes(rt, ora, fmt, w, tokens, cap, kind):
     """Decode (one token at a random position), prefill batches, ragged widths,
-    positions past the capacity (skipped), adversarial blocks."""
+    positions past the capacity (skipped), adversarial blocks, and NaN blocks
+    and rows (the encoders' maximum starts at 0, as the reference's does)."""
     r = np.random.default_rng(w * 7 + tokens + cap)
     key, value = _values(r, tokens, w, kind), _values(r, tokens, w, kind)
     pos = r.permutation(max(cap, tokens))[:tokens].astype(np.uint32) if tokens > 1 else \
@@ -82,7 +95,7 @@ def test_kv_append_shapes(rt, ora, fmt, w, tokens, cap, kind):
     for vnorm in (True, False):
         say(f"kv {fmt} w={w} tokens={tokens} capacity={cap} {kind} vnorm={vnorm}")
         got, exp, _ = run(rt, ora, fmt, key, value, w, cap, pos, vnorm)
-        assert_cache(f"{fmt} w={w} tokens={tokens}", got, exp)
+        assert_cache(f"{fmt} w={w} tokens={tokens}", got, exp, fmt)
 
 
 def test_kv_append_invalid_input(rt):

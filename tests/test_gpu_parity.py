@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 
 import cases
+from cases import assert_bits, assert_bits_nan_equal
 from atlas_amd import rope_tables_gemma4, rope_tables_llama
 from atlas_amd import workloads as wl
 
@@ -26,20 +27,6 @@ f32 = np.float32
 def say(msg):
     print(f"[gpu-parity] {msg}", flush=True)
     sys.stdout.flush()
-
-
-def assert_bits(name, got, exp):
-    assert len(got) == len(exp), name
-    for i, (g, e) in enumerate(zip(got, exp)):
-        g, e = np.asarray(g).reshape(-1), np.asarray(e).reshape(-1)
-        assert g.shape == e.shape, (name, i, g.shape, e.shape)
-        gb, eb = g.view(np.uint8), e.view(np.uint8)
-        if not np.array_equal(gb, eb):
-            gf, ef = g.astype(np.float64), e.astype(np.float64)
-            mism = np.nonzero((g != e) & ~(np.isnan(gf) & np.isnan(ef)))[0]
-            j = mism[0] if mism.size else 0
-            raise AssertionError(f"{name}[{i}]: {mism.size} of {g.size} elements differ; first at {j}: "
-                                 f"gpu={g[j]!r} oracle={e[j]!r} max_abs={np.nanmax(np.abs(gf - ef)):.3e}")
 
 
 def run_golden(rt, ora, name, gpu_fn):
@@ -373,61 +360,6 @@ def test_wide_reduction_is_tolerance_level(rt, ora):
         rt.set_reduction(ATLAS_REDUCTION_SEQUENTIAL)
 
 
-def _adversarial_rows(rows, hidden, seed):
-    """Rows that stress the exact wave-parallel fold of the sum of squares:
-    rounding ties, binade crossings, zeros, subnormal and overflowing squares,
-    non-finite values, wide exponent ranges and a sum that grows through many
-    binades."""
-    r = np.random.default_rng(seed)
-    x = r.standard_normal((rows, hidden)).astype(f32)
-    for i in range(rows):
-        kind = i % 16
-        row = x[i]
-        if kind == 1:
-            row *= f32(1e-20)                                   # subnormal squares
-        elif kind == 2:
-            row *= f32(1e18)                                    # sum overflows to inf
-        elif kind == 3:
-            row[r.random(hidden) < 0.5] = 0.0                   # many zeros
-        elif kind == 4:
-            row[:] = np.trunc(row * 4) / 4                      # coarse values: many exact ties
-        elif kind == 5:
-            row[7] = np.inf
-        elif kind == 6:
-            row[hidden // 3] = np.nan
-        elif kind == 7:
-            row[:] = 1.0
-        elif kind == 8:
-            row[:] = (np.arange(hidden) % 7) * f32(0.5)
-        elif kind == 9:
-            row[:100] *= f32(1e-3)                              # slow start
-        elif kind == 10:
-            row[:] = np.ldexp(1.0 + r.random(hidden), r.integers(-20, 20, hidden)).astype(f32)
-        elif kind == 11:
-            row[:] = 0.0
-        elif kind == 12:
-            row[:] = np.sqrt(np.ldexp(1.0, r.integers(0, 8, hidden))).astype(f32)
-        elif kind == 13:
-            row *= f32(1e-6)
-        elif kind == 14:
-            row[:] = np.trunc(row * 64) / 64
-        elif kind == 15:
-            # squares growing geometrically 1 .. 2^16: the sum climbs past the
-            # four binades the decode-batch fold scans ahead, mid-row
-            row[:] = np.sqrt(np.exp2(np.arange(hidden) * (16.0 / hidden))).astype(f32)
-    return x.reshape(-1)
-
-
-def _assert_bits_nan_equal(name, got, exp):
-    for i, (g, e) in enumerate(zip(got, exp)):
-        g, e = np.asarray(g).reshape(-1), np.asarray(e).reshape(-1)
-        same = (g.view(np.uint32) == e.view(np.uint32)) | (np.isnan(g) & np.isnan(e))
-        if not same.all():
-            j = int(np.nonzero(~same)[0][0])
-            raise AssertionError(f"{name}[{i}]: {int((~same).sum())} of {g.size} differ; first at {j}: "
-                                 f"gpu={g[j]!r} oracle={e[j]!r}")
-
-
 @pytest.mark.parametrize("rows", [2048 + 48, 1024 + 16])
 @pytest.mark.parametrize("hidden", [1536, 2048, 576, 1024, 260])
 @pytest.mark.parametrize("mode", ["plain", "residual", "addnorm", "addscale"])
@@ -440,9 +372,9 @@ def test_rms_exact_fold_adversarial_rows(rt, ora, rows, hidden, mode):
     RMSNorm keeps the chunked parallel fold and the epilogue modes fold in order
     with two rows per wavefront (and a ragged tail)."""
     inp, m = cases.rms_case(rows, hidden, 1e-6, 4000 + hidden, mode)
-    inp["x"] = _adversarial_rows(rows, hidden, 5000 + hidden)
+    inp["x"] = cases.adversarial_rows(rows, hidden, 5000 + hidden)
     say(f"rms exact fold adversarial {mode} rows={rows} hidden={hidden}")
-    _assert_bits_nan_equal(f"rms_{mode}", cases.rms_gpu(rt, inp, m), cases.rms_oracle(ora, inp, m))
+    assert_bits_nan_equal(f"rms_{mode}", cases.rms_gpu(rt, inp, m), cases.rms_oracle(ora, inp, m))
 
 
 @pytest.mark.parametrize("rows,hidden", [(1, 8), (33, 576), (2050, 2048), (7, 4096), (19, 2056), (5, 1000),
@@ -455,34 +387,12 @@ def test_f16_norms_shapes(rt, ora, rows, hidden):
     assert_bits("f16 norms", cases.f16_norm_gpu(rt, inp, m), cases.f16_norm_oracle(ora, inp, m))
 
 
-def _adversarial_f16_rows(rows, hidden, seed):
-    """FP16 rows built to break a reordered or wave-parallel fold: squares of f16
-    values have few significant bits, so exact rounding ties are frequent; plus
-    binade crossings from tiny to large sums, subnormal and zero stretches,
-    mixed magnitudes, and inf / NaN."""
-    r = np.random.default_rng(seed)
-    x = r.standard_normal((rows, hidden)).astype(np.float16)
-    kind = np.arange(rows) % 7
-    few = np.array([0.5, 1.0, 1.5, 2.0, 2.5, 3.0, 0.75, 1.25], np.float16)
-    x[kind == 1] = r.choice(few, (int((kind == 1).sum()), hidden)) * r.choice([-1, 1], (int((kind == 1).sum()), hidden))
-    x[kind == 2] = (r.standard_normal((int((kind == 2).sum()), hidden)) * 1e-6).astype(np.float16)   # subnormal f16
-    big = kind == 3
-    x[big] = (r.standard_normal((int(big.sum()), hidden)) * np.where(r.random((int(big.sum()), hidden)) < 0.1, 3e3, 1e-2)
-              ).astype(np.float16)
-    sparse = kind == 4
-    x[sparse] = np.where(r.random((int(sparse.sum()), hidden)) < 0.05, x[sparse], np.float16(0))
-    x[kind == 5, hidden // 3] = np.float16(np.inf)
-    x[kind == 6, hidden // 2] = np.float16(np.nan)
-    return x.reshape(-1).view(np.uint16)
-
-
 @pytest.mark.parametrize("rows,hidden", [(2048 + 37, 2048), (512 + 5, 2048), (300, 4096), (77, 1536)])
 def test_f16_norm_exact_fold_adversarial_rows(rt, ora, rows, hidden):
-    """The FP16 register engine's fold (in order, or the exact wave-parallel
-    continuations under ATLAS_NORM_PAR_FOLD=1/2) against the oracle's sequential
+    """The FP16 register engine's in-order fold against the oracle's sequential
     sum on adversarial f16 rows, both the plain and the add+norm form."""
     inp, m = cases.f16_norm_case(rows, hidden, 1e-5, 7100 + rows + hidden)
-    inp["x"] = _adversarial_f16_rows(rows, hidden, 7200 + hidden)
+    inp["x"] = cases.adversarial_f16_rows(rows, hidden, 7200 + hidden)
     say(f"f16 norms adversarial rows={rows} hidden={hidden}")
     got, exp = cases.f16_norm_gpu(rt, inp, m), cases.f16_norm_oracle(ora, inp, m)
     for name, g, e in zip(("residual_out", "add+norm", "norm"), got, exp):

@@ -229,6 +229,77 @@ def test_rope_angle_kats(ora):
     assert np.all(c2[0] == 1.0) and np.all(s2[0] == 0.0)
 
 
+def _angle_closed_form(pos, pairs, rotary, theta, factors):
+    """theta_p = pos / theta^(2p/rotary) / factor_p in float64
+    (gemma4_executor.rs:622-633; executor.rs:632-647 with rotary = head_dim)."""
+    p = np.arange(pairs, dtype=np.float64)
+    ang = pos.astype(np.float64)[:, None] / np.power(np.float64(theta), 2.0 * p / rotary)[None, :]
+    return ang / factors.astype(np.float64)[None, :]
+
+
+def _check_tables(cos, sin, pos, pairs, rotary, theta, factors):
+    """Angles within 2 f32 ulp of the closed form on every pair 1..rotary/2-1;
+    cos/sin within 1e-6 of float64 cos/sin of the table's own f32 angle."""
+    exact = _angle_closed_form(pos, pairs, rotary, theta, factors)[:, 1:]
+    # recover the f32 angle the table was built from: the closed form rounded to
+    # f32 is within 2 ulp of it, so check cos/sin of that angle and of its
+    # neighbours, and the angle itself through the closed form
+    a32 = exact.astype(np.float32)
+    spacing = np.spacing(np.abs(a32)).astype(np.float64)
+    c, s = cos[:, 1:].astype(np.float64), sin[:, 1:].astype(np.float64)
+    best = np.full(exact.shape, np.inf)
+    for k in range(-2, 3):
+        cand = a32.astype(np.float64) + k * spacing
+        err = np.maximum(np.abs(c - np.cos(cand)), np.abs(s - np.sin(cand)))
+        best = np.minimum(best, err)
+    return float(best.max())
+
+
+def test_rope_tables_angle_against_float64_closed_form(ora):
+    """Pins the angle exponent (2p/rotary) on every pair > 0, which the pair-0
+    KATs cannot see: table entries equal cos/sin of an f32 angle within 2 ulp
+    of pos / theta^(2p/rotary) / factor (float64), at positions up to 131071,
+    theta 1e4 / 1e6 / 130000, rotary 128 / 256 / 512, unit and non-unit
+    per-pair factors.  A planted exponent p/rotary must fail the same check."""
+    r = np.random.default_rng(41)
+    pos = np.concatenate([np.array([1, 2, 3, 7, 100, 4095, 65535, 131071]),
+                          r.integers(0, 131072, 24)]).astype(np.uint32)
+    for rotary in (128, 256, 512):
+        pairs = rotary // 2
+        for theta in (1e4, 1e6, 130000.0):
+            for factors in (np.ones(pairs, f32), r.uniform(0.5, 40.0, pairs).astype(f32)):
+                c, s = ora.rope_tables_gemma4(pos, pairs, rotary, theta, factors)
+                assert _check_tables(c, s, pos, pairs, rotary, theta, factors) < 1e-6, (rotary, theta)
+        c, s = ora.rope_tables_llama(pos, rotary, 130000.0)
+        assert _check_tables(c, s, pos, pairs, rotary, 130000.0, np.ones(pairs, f32)) < 1e-6
+    # planted mistake: exponent p/rotary instead of 2p/rotary
+    pairs, rotary, theta = 128, 256, 1e6
+    p = np.arange(pairs, dtype=np.float32)
+    wrong = pos.astype(np.float32)[:, None] / np.power(np.float32(theta), p / np.float32(rotary))[None, :]
+    assert _check_tables(np.cos(wrong), np.sin(wrong), pos, pairs, rotary, theta, np.ones(pairs, f32)) > 1e-2
+    # planted mistake: factor multiplied instead of divided
+    ff = r.uniform(0.5, 40.0, pairs).astype(f32)
+    c, s = ora.rope_tables_gemma4(pos, pairs, rotary, theta, np.ones(pairs, f32))
+    ang = _angle_closed_form(pos, pairs, rotary, theta, np.ones(pairs, f32)) * ff.astype(np.float64)[None, :]
+    assert _check_tables(np.cos(ang), np.sin(ang), pos, pairs, rotary, theta, ff) > 1e-2
+
+
+def test_rope_angle_scalar_matches_closed_form(ora):
+    """The scalar angle (the decode path's per-token entry) is within 2 f32
+    ulp of the float64 closed form on pairs > 0 and is 0 from rotary/2 up."""
+    r = np.random.default_rng(43)
+    for _ in range(400):
+        rotary = int(r.choice([128, 256, 512]))
+        pair = int(r.integers(1, rotary // 2))
+        pos = int(r.integers(0, 131072))
+        theta = float(r.choice([1e4, 1e6, 130000.0]))
+        factor = float(np.float32(r.uniform(0.5, 40.0)))
+        got = ora.rope_angle(pos, pair, rotary, theta, factor)
+        exact = pos / theta ** (2.0 * pair / rotary) / factor
+        assert abs(got - exact) <= 2 * np.spacing(np.float32(abs(exact))), (pos, pair, rotary, theta, factor)
+        assert ora.rope_angle(pos, rotary // 2 + pair % 7, rotary, theta, factor) == 0.0
+
+
 def test_rope_half_equals_reference_three_kernel_chain(ora):
     """rope_half_to_interleaved -> rope_f32 -> rope_interleaved_to_half (kernels.metal:940-994)."""
     r = np.random.default_rng(14)
@@ -247,6 +318,72 @@ def test_rope_half_equals_reference_three_kernel_chain(ora):
     n_out = got[..., : d // 2] ** 2 + got[..., d // 2:] ** 2
     assert np.allclose(n_in, n_out, rtol=1e-5)
     assert np.array_equal(got[0], x[0])
+
+
+def _np_rope_half_f16(x16, c, s, tokens, heads, d, stride):
+    """numpy restatement: widen f16 exactly, rotate with separately rounded f32
+    products and one f32 add/subtract, round once to f16 (IEEE RNE)."""
+    x = x16.view(np.float16).astype(f32).reshape(tokens, heads, d)
+    cc = c.reshape(tokens, stride)[:, None, : d // 2].astype(f32)
+    ss = s.reshape(tokens, stride)[:, None, : d // 2].astype(f32)
+    x0, x1 = x[..., : d // 2], x[..., d // 2:]
+    with np.errstate(invalid="ignore", over="ignore"):
+        lo = (x0 * cc).astype(f32) - (x1 * ss).astype(f32)
+        hi = (x0 * ss).astype(f32) + (x1 * cc).astype(f32)
+    return np.concatenate([lo, hi], -1).astype(np.float16).view(np.uint16).reshape(-1)
+
+
+def test_rope_half_f16_is_widen_rotate_round(ora):
+    """oracle_rope_half_f16 == f32_to_f16(rope_half(f16_to_f32(x))) bit for bit
+    at the C2 shape [2048, 32, 64] (theta 130000), and equals an independent
+    numpy restatement of the same steps.  The f32 rotation it composes is
+    pinned by the reference three-kernel chain and the cpu_rope KAT above.
+    Planted mistakes (products rounded to f16 before the subtraction; the
+    pair partner taken from the wrong half) must fail."""
+    r = np.random.default_rng(19)
+    tokens, heads, d = 2048, 32, 64
+    x16 = r.standard_normal(tokens * heads * d).astype(np.float16).view(np.uint16)
+    # adversarial rows: exact cancellation, f16 subnormals, the f16 max, inf, nan
+    x16[:64] = np.float16(1.0).view(np.uint16)
+    x16[64:128] = np.array([6.0e-8, -6.0e-8, 65504.0, -65504.0] * 16, np.float16).view(np.uint16)
+    x16[128:130] = np.array([np.inf, np.nan], np.float16).view(np.uint16)
+    c, s = ora.rope_tables_llama(np.arange(tokens, dtype=np.uint32), d, 130000.0)
+    got = ora.rope_half_f16(x16, c, s, tokens, heads, d, d // 2)
+    composed = ora.f32_to_f16(ora.rope_half(ora.f16_to_f32(x16), c, s, tokens, heads, d, d // 2))
+    assert np.array_equal(got, composed)
+    ref = _np_rope_half_f16(x16, c, s, tokens, heads, d, d // 2)
+    nan = np.isnan(ref.view(np.float16))
+    assert np.array_equal(np.isnan(got.view(np.float16)), nan)
+    assert np.array_equal(got[~nan], ref[~nan])
+    # within one f16 ulp of the float64 rotation of the same f32 tables, plus
+    # the f32 arithmetic's own bound (2^-23 of the operand magnitudes) where
+    # the two products cancel
+    x64 = x16.view(np.float16).astype(np.float64).reshape(tokens, heads, d)
+    c64 = c.astype(np.float64)[:, None, :]
+    s64 = s.astype(np.float64)[:, None, :]
+    with np.errstate(invalid="ignore", over="ignore"):
+        a0, a1 = x64[..., :32], x64[..., 32:]
+        exact = np.concatenate([a0 * c64 - a1 * s64, a0 * s64 + a1 * c64], -1)
+        mag = np.concatenate([np.abs(a0 * c64) + np.abs(a1 * s64), np.abs(a0 * s64) + np.abs(a1 * c64)], -1)
+        g = got.view(np.float16).astype(np.float64).reshape(exact.shape)
+        fin = np.isfinite(exact) & (np.abs(exact) < 65504)
+        bound = np.spacing(np.abs(exact[fin]).astype(np.float16)).astype(np.float64) + 2.0 ** -23 * mag[fin]
+    assert np.all(np.abs(g[fin] - exact[fin]) <= bound)
+    with np.errstate(invalid="ignore", over="ignore"):
+        # planted: each product rounded to f16 before the subtraction
+        x = x16.view(np.float16).astype(f32).reshape(tokens, heads, d)
+        cc, ss = c[:, None, :].astype(f32), s[:, None, :].astype(f32)
+        r16 = lambda v: v.astype(np.float16).astype(f32)
+        lo = r16(x[..., :32] * cc) - r16(x[..., 32:] * ss)
+        hi = r16(x[..., :32] * ss) + r16(x[..., 32:] * cc)
+        planted = np.concatenate([lo, hi], -1).astype(np.float16).view(np.uint16).reshape(-1)
+        assert not np.array_equal(got[~nan], planted[~nan])
+        # planted: interleaved partner (x[2p], x[2p+1]) instead of the half split
+        xi = x.reshape(tokens, heads, 32, 2)
+        lo = xi[..., 0] * cc - xi[..., 1] * ss
+        hi = xi[..., 0] * ss + xi[..., 1] * cc
+        planted = np.concatenate([lo, hi], -1).astype(np.float16).view(np.uint16).reshape(-1)
+        assert not np.array_equal(got[~nan], planted[~nan])
 
 
 def test_qk_norm_rope_equals_norm_then_rope(ora):
