@@ -109,6 +109,7 @@ SIGNATURES = {
     "atlas_hip_embed_f32": [CTX, P, P, P, U32, U32, U32, F],
     "atlas_hip_embed_q4_0": [CTX, P, P, P, U32, U32, U32, F],
     "atlas_hip_embed_q6_k": [CTX, P, P, P, U32, U32, U32, F],
+    "atlas_hip_embed_q8_0": [CTX, P, P, P, U32, U32, U32, F],
     "atlas_hip_ple_q4_0": [CTX, P, P, P, P, U32, U32, U32, U32, F, F],
     "atlas_hip_ple_q6_k": [CTX, P, P, P, P, U32, U32, U32, U32, F, F],
     "atlas_hip_matvec_q4_0_rms_f32": [CTX, P, P, P, U32, U32, P, F],

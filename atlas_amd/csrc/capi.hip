@@ -636,19 +636,22 @@ int atlas_hip_embed_f32(atlas_hip_ctx* ctx, const float* table, const uint32_t* 
                     "embed_f32");
 }
 
-static int embed_quant(atlas_hip_ctx* ctx, int q6, const uint8_t* table, const uint32_t* ids, float* output,
+// format: 0 Q4_0, 1 Q6_K, 2 Q8_0 (atlas::launch_embed_quant)
+static int embed_quant(atlas_hip_ctx* ctx, int format, const uint8_t* table, const uint32_t* ids, float* output,
                        uint32_t vocab, uint32_t hidden, uint32_t tokens, float scale) {
+    static const char* const kNames[] = {"embed_q4_0", "embed_q6_k", "embed_q8_0"};
+    static const char* const kBad[] = {"Q4_0 embedding dimensions or token IDs are invalid",
+                                       "Q6_K embedding dimensions or token IDs are invalid",
+                                       "Q8_0 embedding dimensions or token IDs are invalid"};
     int rc = enter(ctx);
     if (rc) return rc;
-    const uint32_t qk = q6 ? 256 : 32;
+    const uint32_t qk = format == 1 ? 256 : 32;
     if (!table || !ids || !output) return invalid(ctx, "quantized embedding buffer is null");
-    if (hidden == 0 || hidden % qk != 0 || tokens == 0 || hidden > 65536)
-        return invalid(ctx, q6 ? "Q6_K embedding dimensions or token IDs are invalid"
-                               : "Q4_0 embedding dimensions or token IDs are invalid");
+    if (hidden == 0 || hidden % qk != 0 || tokens == 0 || hidden > 65536) return invalid(ctx, kBad[format]);
     if (!aligned16(output)) return invalid(ctx, "embedding output must be 16-byte aligned");
     return launched(ctx,
-                    atlas::launch_embed_quant(ctx->stream, q6, table, ids, output, vocab, hidden, tokens, scale),
-                    q6 ? "embed_q6_k" : "embed_q4_0");
+                    atlas::launch_embed_quant(ctx->stream, format, table, ids, output, vocab, hidden, tokens, scale),
+                    kNames[format]);
 }
 
 int atlas_hip_embed_q4_0(atlas_hip_ctx* ctx, const uint8_t* table, const uint32_t* ids, float* output,
@@ -661,6 +664,11 @@ int atlas_hip_embed_q6_k(atlas_hip_ctx* ctx, const uint8_t* table, const uint32_
     return embed_quant(ctx, 1, table, ids, output, vocab, hidden, tokens, scale);
 }
 
+int atlas_hip_embed_q8_0(atlas_hip_ctx* ctx, const uint8_t* table, const uint32_t* ids, float* output,
+                         uint32_t vocab, uint32_t hidden, uint32_t tokens, float scale) {
+    return embed_quant(ctx, 2, table, ids, output, vocab, hidden, tokens, scale);
+}
+
 static int ple(atlas_hip_ctx* ctx, int q6, const uint8_t* table, const uint32_t* ids, const float* projection,
                float* output, uint32_t vocab, uint32_t layers, uint32_t width, uint32_t tokens, float es, float os) {
     int rc = enter(ctx);
@@ -670,6 +678,7 @@ static int ple(atlas_hip_ctx* ctx, int q6, const uint8_t* table, const uint32_t*
     if (!table || !ids || !projection || !output) return invalid(ctx, "PLE buffer is null");
     if (layers == 0 || width == 0 || tokens == 0 || row % qk != 0)
         return invalid(ctx, "PLE dimensions are invalid");
+    if (vocab == 0) return invalid(ctx, "PLE table has no rows (vocab is 0)");
     if (row > 16384) return invalid(ctx, "PLE rows are limited to 16384 values (layers * width)");
     if (!aligned16(projection) || !aligned16(output)) return invalid(ctx, "PLE projection/output must be 16-byte aligned");
     return launched(ctx,

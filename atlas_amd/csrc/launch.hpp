@@ -92,7 +92,9 @@ hipError_t launch_geglu_offset_f32(hipStream_t stream, const float* gate, const 
 hipError_t launch_embed_f32(hipStream_t stream, const float* table, const uint32_t* ids,
                             float* out, uint32_t vocab, uint32_t hidden, uint32_t tokens,
                             float scale);
-hipError_t launch_embed_quant(hipStream_t stream, int q6k, const uint8_t* table,
+// format: 0 Q4_0 (18-byte blocks of 32), 1 Q6_K (210-byte blocks of 256),
+// 2 Q8_0 (34-byte blocks of 32).  Rows with id >= vocab are left untouched.
+hipError_t launch_embed_quant(hipStream_t stream, int format, const uint8_t* table,
                               const uint32_t* ids, float* out, uint32_t vocab, uint32_t hidden,
                               uint32_t tokens, float scale);
 hipError_t launch_ple_quant(hipStream_t stream, int q6k, const uint8_t* table, const uint32_t* ids,

@@ -265,6 +265,9 @@ class HipRuntime:
     def embed_q6_k(self, table, ids, out, vocab, hidden, tokens, scale):
         self._check(self.lib.atlas_hip_embed_q6_k(self.ctx, _ptr(table), _ptr(ids), _ptr(out), vocab, hidden, tokens, scale))
 
+    def embed_q8_0(self, table, ids, out, vocab, hidden, tokens, scale=1.0):
+        self._check(self.lib.atlas_hip_embed_q8_0(self.ctx, _ptr(table), _ptr(ids), _ptr(out), vocab, hidden, tokens, scale))
+
     def ple_q4_0(self, table, ids, proj, out, vocab, layers, width, tokens, emb_scale, out_scale):
         self._check(self.lib.atlas_hip_ple_q4_0(self.ctx, _ptr(table), _ptr(ids), _ptr(proj), _ptr(out), vocab, layers,
                                                 width, tokens, emb_scale, out_scale))

@@ -57,6 +57,15 @@ def q6_k_table(r: np.random.Generator, vocab: int, hidden: int) -> np.ndarray:
     return table.reshape(-1)
 
 
+def q8_0_table(r: np.random.Generator, vocab: int, hidden: int) -> np.ndarray:
+    """Q8_0 rows [vocab, hidden/32 blocks x 34 B]: f16 d ~ U(0.001, 0.05) (IEEE RNE) + 32 random int8."""
+    blocks = hidden // 32
+    table = np.frombuffer(r.bytes(vocab * blocks * 34), dtype=np.uint8).reshape(vocab, blocks, 34).copy()
+    d = r.uniform(0.001, 0.05, size=(vocab, blocks)).astype(np.float16)
+    table[:, :, 0:2] = d.view(np.uint8).reshape(vocab, blocks, 2)
+    return table.reshape(-1)
+
+
 def q_row_bytes(hidden: int, q6: bool) -> int:
     return (hidden // 256) * 210 if q6 else (hidden // 32) * 18
 

@@ -273,6 +273,14 @@ int atlas_hip_embed_q4_0(atlas_hip_ctx *ctx, const uint8_t *table, const uint32_
 int atlas_hip_embed_q6_k(atlas_hip_ctx *ctx, const uint8_t *table, const uint32_t *ids,
                          float *output, uint32_t vocab, uint32_t hidden, uint32_t tokens,
                          float scale);
+/* embedding_lookup_q8_0 (kernels.metal:658-661): the Llama resident
+ * embedding of Q8_0 tables (resident_embedding_kernel, crates/atlas-model/
+ * src/executor.rs:1541-1549, dispatched at :1063-1074, scale 1.0).  34-byte
+ * blocks of 32 (f16 d, 32 int8); out = f32(int8) * d * scale.  hidden % 32
+ * == 0; rows whose id >= vocab are left untouched; output 16-byte aligned. */
+int atlas_hip_embed_q8_0(atlas_hip_ctx *ctx, const uint8_t *table, const uint32_t *ids,
+                         float *output, uint32_t vocab, uint32_t hidden, uint32_t tokens,
+                         float scale);
 /* Gemma PLE chain gather + x sqrt(256) + add + x 1/sqrt(2)
  * (gemma4_executor.rs:3555-3631, 4162-4237; gemma4_combine_ple
  * crates/atlas-model/src/lib.rs:206-219):

@@ -483,6 +483,13 @@ void oracle_dequant_q4_0_block(const uint8_t *block, float *out32) {
     }
 }
 
+/* Q8_0 (crates/atlas-core/src/gguf.rs:431-435): 34-byte block = f16 d (LE)
+ * then 32 signed bytes; v = f32((int8)q) * d (exact in f32: 8 x 11 bits). */
+void oracle_dequant_q8_0_block(const uint8_t *block, float *out32) {
+    float d = oracle_f16_to_f32((uint16_t)(block[0] | (block[1] << 8)));
+    for (int i = 0; i < 32; ++i) out32[i] = (float)(int8_t)block[2 + i] * d;
+}
+
 /* Q6_K (crates/atlas-core/src/gguf.rs:384-413): 210-byte super-block =
  * ql[128] | qh[64] | scales[16] (i8) | d (f16 at byte 208).  For i < 256:
  * half = i/128, w = i%128, stream = w/32, lane = w%32;
@@ -545,6 +552,23 @@ void oracle_embed_q4_0(const uint8_t *table, const uint32_t *ids, float *output,
         if (id >= vocab) continue;
         for (size_t b = 0; b < blocks; ++b) {
             oracle_dequant_q4_0_block(table + ((size_t)id * blocks + b) * 18, tmp);
+            for (int i = 0; i < 32; ++i) output[t * hidden + b * 32 + i] = tmp[i] * scale;
+        }
+    }
+}
+
+/* embedding_lookup_q8_0 (kernels.metal:658-661; the Llama resident embedding
+ * for Q8_0 tables, crates/atlas-model/src/executor.rs:1541-1549), then the
+ * optional scalar_multiply_f32 by `scale` (1 for the Llama path). */
+void oracle_embed_q8_0(const uint8_t *table, const uint32_t *ids, float *output, size_t vocab,
+                       size_t hidden, size_t tokens, float scale) {
+    size_t blocks = hidden / 32;
+    float tmp[32];
+    for (size_t t = 0; t < tokens; ++t) {
+        uint32_t id = ids[t];
+        if (id >= vocab) continue;
+        for (size_t b = 0; b < blocks; ++b) {
+            oracle_dequant_q8_0_block(table + ((size_t)id * blocks + b) * 34, tmp);
             for (int i = 0; i < 32; ++i) output[t * hidden + b * 32 + i] = tmp[i] * scale;
         }
     }

@@ -124,11 +124,14 @@ void oracle_geglu_offset_f32(const float *gate, const float *ple,
 
 /* ---- gathers and block dequant ------------------------------------------ */
 void oracle_dequant_q4_0_block(const uint8_t *block, float *out32);
+void oracle_dequant_q8_0_block(const uint8_t *block, float *out32);
 void oracle_dequant_q6_k_block(const uint8_t *block, float *out256);
 void oracle_dequant_q6_k_block_llama_order(const uint8_t *block, float *out256);
 void oracle_embed_f32(const float *table, const uint32_t *ids, float *output,
                       size_t vocab, size_t hidden, size_t tokens);
 void oracle_embed_q4_0(const uint8_t *table, const uint32_t *ids, float *output,
+                       size_t vocab, size_t hidden, size_t tokens, float scale);
+void oracle_embed_q8_0(const uint8_t *table, const uint32_t *ids, float *output,
                        size_t vocab, size_t hidden, size_t tokens, float scale);
 void oracle_embed_q6_k(const uint8_t *table, const uint32_t *ids, float *output,
                        size_t vocab, size_t hidden, size_t tokens, float scale);

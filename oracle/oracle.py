@@ -50,10 +50,12 @@ _SIGS = {
     "oracle_geglu_f32": ([P, P, P, SZ], None),
     "oracle_geglu_offset_f32": ([P, P, P, SZ, SZ, SZ, SZ], None),
     "oracle_dequant_q4_0_block": ([P, P], None),
+    "oracle_dequant_q8_0_block": ([P, P], None),
     "oracle_dequant_q6_k_block": ([P, P], None),
     "oracle_dequant_q6_k_block_llama_order": ([P, P], None),
     "oracle_embed_f32": ([P, P, P, SZ, SZ, SZ], None),
     "oracle_embed_q4_0": ([P, P, P, SZ, SZ, SZ, F], None),
+    "oracle_embed_q8_0": ([P, P, P, SZ, SZ, SZ, F], None),
     "oracle_embed_q6_k": ([P, P, P, SZ, SZ, SZ, F], None),
     "oracle_ple_q4_0": ([P, P, P, P, SZ, SZ, SZ, SZ, F, F], None),
     "oracle_ple_q6_k": ([P, P, P, P, SZ, SZ, SZ, SZ, F, F], None),
@@ -276,6 +278,13 @@ def dequant_q4_0_block(block):
     return out
 
 
+def dequant_q8_0_block(block):
+    b = _c(block, u8)
+    out = np.empty(32, f32)
+    lib().oracle_dequant_q8_0_block(_p(b), _p(out))
+    return out
+
+
 def dequant_q6_k_block(block, llama_order=False):
     b = _c(block, u8)
     out = np.empty(256, f32)
@@ -295,6 +304,13 @@ def embed_q4_0(table, ids, vocab, hidden, scale, out=None):
     t, i = _c(table, u8), _c(ids, u32)
     out = np.zeros(i.size * hidden, f32) if out is None else np.array(out, f32, copy=True)
     lib().oracle_embed_q4_0(_p(t), _p(i), _p(out), vocab, hidden, i.size, scale)
+    return out
+
+
+def embed_q8_0(table, ids, vocab, hidden, scale, out=None):
+    t, i = _c(table, u8), _c(ids, u32)
+    out = np.zeros(i.size * hidden, f32) if out is None else np.array(out, f32, copy=True)
+    lib().oracle_embed_q8_0(_p(t), _p(i), _p(out), vocab, hidden, i.size, scale)
     return out
 
 

@@ -150,16 +150,20 @@ def glu_gpu(rt, inp, m):
     return [o.download(m["n"])]
 
 
-def embed_q_case(vocab, hidden, tokens, seed, q6):
+def embed_q_case(vocab, hidden, tokens, seed, q6, fmt=None):
+    """Token gather from a packed table: fmt "q4_0", "q6_k" (q6=True) or "q8_0"."""
+    fmt = fmt or ("q6_k" if q6 else "q4_0")
     r = wl.rng(seed)
-    table = wl.q6_k_table(r, vocab, hidden) if q6 else wl.q4_0_table(r, vocab, hidden)
+    make = {"q4_0": wl.q4_0_table, "q6_k": wl.q6_k_table, "q8_0": wl.q8_0_table}[fmt]
+    table = make(r, vocab, hidden)
     ids = wl.token_ids(r, tokens, vocab)
-    return {"table": table, "ids": ids}, dict(vocab=vocab, hidden=hidden, tokens=tokens, q6=q6,
-                                              scale=float(wl.f32_sqrt(hidden)))
+    return {"table": table, "ids": ids}, dict(vocab=vocab, hidden=hidden, tokens=tokens, q6=fmt == "q6_k",
+                                              fmt=fmt, scale=float(wl.f32_sqrt(hidden)))
 
 
 def embed_q_oracle(ora, inp, m):
-    fn = ora.embed_q6_k if m["q6"] else ora.embed_q4_0
+    fn = {"q4_0": ora.embed_q4_0, "q6_k": ora.embed_q6_k, "q8_0": ora.embed_q8_0}[m.get("fmt", "q6_k" if m["q6"]
+                                                                                    else "q4_0")]
     return [fn(inp["table"], inp["ids"], m["vocab"], m["hidden"], m["scale"])]
 
 
@@ -168,7 +172,9 @@ def embed_q_gpu(rt, inp, m):
     n = m["tokens"] * m["hidden"]
     o = rt.empty(n)
     rt.memset(o, 0, n * 4)
-    (rt.embed_q6_k if m["q6"] else rt.embed_q4_0)(t, ids, o, m["vocab"], m["hidden"], m["tokens"], m["scale"])
+    fn = {"q4_0": rt.embed_q4_0, "q6_k": rt.embed_q6_k, "q8_0": rt.embed_q8_0}[m.get("fmt", "q6_k" if m["q6"]
+                                                                                   else "q4_0")]
+    fn(t, ids, o, m["vocab"], m["hidden"], m["tokens"], m["scale"])
     rt.sync()
     return [o.download(n)]
 

@@ -51,10 +51,15 @@ def assert_same(got, exp, tag):
             assert np.array_equal(g.view(np.uint32), np.asarray(e).view(np.uint32)), f"{tag}: {key}[{layer}]"
 
 
-def test_decode_step_eager_and_graph_replays(rt, ora):
-    shape = wl.DecodeShape(batch=64)
-    say(f"building decode step {shape}")
-    step = GemmaDecodeStep(rt, shape, seed=3, vocab=8192)
+@pytest.mark.parametrize("batch,vocab", [(64, 8192), (256, 262144)])
+def test_decode_step_eager_and_graph_replays(rt, ora, batch, vocab):
+    """A small chain, and BASELINE configs[4] at its stated shape: 256
+    sequences at positions drawn from [0, 131072), 35 layers with local and
+    global theta interleaved 4:1, the Gemma vocabulary of 262144 rows for the
+    Q4_0 token and PLE tables."""
+    shape = wl.DecodeShape(batch=batch)
+    say(f"building decode step {shape} vocab={vocab}")
+    step = GemmaDecodeStep(rt, shape, seed=3, vocab=vocab)
     try:
         exp_a = oracle_step(ora, step)
         say("eager step")

@@ -15,7 +15,7 @@ import pytest
 
 import cases
 from cases import assert_bits, assert_bits_nan_equal
-from atlas_amd import rope_tables_gemma4, rope_tables_llama
+from atlas_amd import OperatorError, rope_tables_gemma4, rope_tables_llama
 from atlas_amd import workloads as wl
 
 pytestmark = pytest.mark.gpu
@@ -279,6 +279,47 @@ def test_full_size_gathers_c4(rt, ora):
         assert_bits("embed", cases.embed_q_gpu(rt, inp, m), cases.embed_q_oracle(ora, inp, m))
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q6_k", "q8_0"])
+@pytest.mark.parametrize("hidden,tokens", [(256, 1), (1536, 4097), (2048, 3), (8960, 65), (19968, 9), (20224, 9),
+                                           (28672, 5), (29184, 5), (65536, 3)])
+def test_embed_quant_shapes(rt, ora, fmt, hidden, tokens):
+    """Every packed gather format over row widths that keep four rows per
+    workgroup in LDS and ones that do not (Q6_K > 19968, Q4_0 > 28672 values),
+    ragged grids and the maximum width; ids include the first and last row.
+    Q8_0 is the Llama resident embedding (executor.rs:1541-1549) with the
+    reference's scale of 1; the others are scaled by sqrt(hidden)."""
+    if fmt == "q6_k" and hidden % 256:
+        pytest.skip("Q6_K needs hidden % 256 == 0")
+    vocab = 257
+    inp, m = cases.embed_q_case(vocab, hidden, tokens, 640 + hidden + tokens, fmt == "q6_k", fmt)
+    inp["ids"][0] = vocab - 1
+    if fmt == "q8_0":
+        m["scale"] = 1.0
+    say(f"embed {fmt} hidden={hidden} tokens={tokens}")
+    assert_bits(f"embed {fmt}", cases.embed_q_gpu(rt, inp, m), cases.embed_q_oracle(ora, inp, m))
+
+
+def test_embed_q8_0_out_of_range_and_scale(rt, ora):
+    """Q8_0 ids at and past the vocabulary leave rows untouched
+    (kernels.metal:660); a non-unit scale rounds once after the exact dequant."""
+    vocab, h = 100, 1536
+    ids = np.array([1, 100, 5, 4000000000, 99, 0], np.uint32)
+    inp, m = cases.embed_q_case(vocab, h, ids.size, 650, False, "q8_0")
+    tb, ib = rt.upload(inp["table"]), rt.upload(ids)
+    for scale in (1.0, float(wl.f32_sqrt(h))):
+        sentinel = np.full(ids.size * h, 7.0, f32)
+        ob = rt.upload(sentinel)
+        say(f"embed q8_0 out-of-range ids scale={scale}")
+        rt.embed_q8_0(tb, ib, ob, vocab, h, ids.size, scale)
+        rt.sync()
+        exp = ora.embed_q8_0(inp["table"], ids, vocab, h, scale, out=sentinel)
+        assert_bits("q8_0 oob untouched", [ob.download(ids.size * h)], [exp])
+        assert np.all(exp.reshape(ids.size, -1)[[1, 3]] == 7.0)
+    with pytest.raises(OperatorError) as e:
+        rt.embed_q8_0(tb, ib, rt.empty(ids.size * 48), vocab, 48, ids.size)   # hidden % 32 != 0
+    assert e.value.kind == "InvalidInput"
+
+
 def test_full_size_ple_c4(rt, ora):
     S = wl.QuantGatherShape()
     inp, m = cases.ple_case(S.vocab, S.ple_layers, S.ple_width, S.tokens, 610, False)
@@ -329,6 +370,11 @@ def test_ple_out_of_range_ids_leave_rows_untouched(rt, ora):
         exp = ora.ple(inp["table"], ids, inp["proj"], vocab, layers, width, m["es"], m["os"], q6=q6, out=sentinel)
         assert_bits("ple oob untouched", [ob.download(n)], [exp])
         assert np.all(exp.reshape(ids.size, -1)[[1, 3, 6]] == 7.0)
+        # an empty table (vocab 0) is invalid input: no row may be staged from it
+        say(f"ple vocab 0 q6={q6}")
+        with pytest.raises(OperatorError) as e:
+            (rt.ple_q6_k if q6 else rt.ple_q4_0)(tb, ib, pb, ob, 0, layers, width, ids.size, m["es"], m["os"])
+        assert e.value.kind == "InvalidInput"
 
 
 def test_wide_reduction_is_tolerance_level(rt, ora):

@@ -444,6 +444,43 @@ def test_q6_k_reference_kat_and_independent_decoder(ora):
         assert np.array_equal(ora.dequant_q6_k_block(blk), ora.dequant_q6_k_block(blk, llama_order=True))
 
 
+def test_q8_0_reference_round_trip_and_brute_force(ora):
+    """q4_and_q8_blocks_round_trip_without_full_dequantization
+    (crates/atlas-core/tests/phase_11a_gguf.rs:33-54): values (i-16)/7 encoded
+    to Q8_0 and decoded stay within 0.03.  Then every int8 code under random
+    f16 scales equals the exact product int8 * f16 (gguf.rs:431-435), and a
+    planted unsigned-byte decode fails."""
+    vals = ((np.arange(32) - 16.0) / 7.0).astype(f32)
+    block = np.zeros(34, np.uint8)
+    ora.lib().oracle_encode_q8_0_block(vals.ctypes.data, block.ctypes.data)
+    dec = ora.dequant_q8_0_block(block)
+    assert np.max(np.abs(dec - vals)) <= 0.03
+    r = np.random.default_rng(31)
+    codes = np.arange(256, dtype=np.uint8)
+    for _ in range(40):
+        d = np.float16(r.uniform(1e-4, 4.0) * r.choice([-1, 1]))
+        for chunk in range(8):
+            b = np.zeros(34, np.uint8)
+            b[0:2] = np.array([d]).view(np.uint8)
+            b[2:] = codes[32 * chunk: 32 * chunk + 32]
+            got = ora.dequant_q8_0_block(b)
+            exact = b[2:].view(np.int8).astype(np.float64) * float(d)
+            assert np.array_equal(got.astype(np.float64), exact)
+            unsigned = b[2:].astype(np.float64) * float(d)
+            if chunk >= 4:   # codes 128..255: the signed reading differs
+                assert not np.array_equal(got.astype(np.float64), unsigned)
+    # the gather: rows by id, ids >= vocab untouched, one rounding by the scale
+    vocab, h = 9, 64
+    table = np.frombuffer(r.bytes(vocab * 2 * 34), np.uint8).copy()
+    table.reshape(vocab, 2, 34)[:, :, 0:2] = np.array([0.125], np.float16).view(np.uint8)
+    ids = np.array([3, 9, 0, 8], np.uint32)
+    got = ora.embed_q8_0(table, ids, vocab, h, 1.5, out=np.full(ids.size * h, -1.0, f32)).reshape(ids.size, h)
+    rows = table.reshape(vocab, 2, 34)[:, :, 2:].view(np.int8).reshape(vocab, h).astype(f32) * f32(0.125)
+    assert np.array_equal(got[0], rows[3] * f32(1.5)) and np.array_equal(got[2], rows[0] * f32(1.5))
+    assert np.all(got[1] == -1.0)
+    assert np.array_equal(got[3], rows[8] * f32(1.5))
+
+
 def test_dequant_brute_force_every_code(ora):
     r = np.random.default_rng(17)
     for d in [np.float16(1.0), np.float16(0.0137), np.float16(-2.5), np.float16(6e-5)]:
