@@ -122,6 +122,7 @@ SIGNATURES = {
     "atlas_hip_softcap_f32": [CTX, P, P, U64, F],
     "atlas_hip_argmax_f32": [CTX, P, P, U32, U32],
     "atlas_hip_softcap_argmax_f32": [CTX, P, P, P, U32, U32, F],
+    "atlas_hip_softcap_argmax_f32_noalloc": [CTX, P, P, P, U32, U32, F],
     "atlas_gguf_open": [c_char_p, POINTER(c_void_p), c_char_p, SZ],
     "atlas_gguf_from_bytes": [P, SZ, POINTER(c_void_p), c_char_p, SZ],
     "atlas_gguf_close": [P],

@@ -15,7 +15,9 @@
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <mutex>
 #include <string>
+#include <vector>
 
 struct atlas_hip_ctx {
     int device = 0;
@@ -26,6 +28,9 @@ struct atlas_hip_ctx {
     // argmax workspace (per-workgroup partial keys of the rows being
     // reduced): allocated once here, never inside an op
     void* argmax_ws = nullptr;
+    // this device's copy of the library's static argmax scratch (the
+    // no-allocation soft cap + argmax entry point); resolved at init
+    void* argmax_scratch = nullptr;
     std::string last_error;
     atlas_hip_telemetry tel{};
 };
@@ -106,6 +111,28 @@ int atlas_hip_device_count(int* count) {
     return ATLAS_OK;
 }
 
+namespace {
+
+// The static scratch's address on each device, resolved once per device (with
+// that device current) and kept for the life of the process.
+hipError_t scratch_address(int device, void** ptr) {
+    static std::mutex m;
+    static std::vector<void*> addr;
+    std::lock_guard<std::mutex> lock(m);
+    if (addr.size() <= static_cast<size_t>(device)) addr.resize(device + 1, nullptr);
+    if (!addr[device]) {
+        void* p = nullptr;
+        const hipError_t e = atlas::argmax_scratch_address(&p);
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        addr[device] = p;
+    }
+    *ptr = addr[device];
+    return hipSuccess;
+}
+
+}  // namespace
+
 int atlas_hip_init(int device, atlas_hip_ctx** out) {
     if (!out) return ATLAS_ERR_INVALID_INPUT;
     *out = nullptr;
@@ -127,6 +154,13 @@ int atlas_hip_init(int device, atlas_hip_ctx** out) {
         (void)hipStreamDestroy(ctx->own_stream);
         delete ctx;
         return e == hipErrorOutOfMemory ? ATLAS_ERR_OUT_OF_MEMORY : ATLAS_ERR_COMMAND_FAILED;
+    }
+    e = scratch_address(device, &ctx->argmax_scratch);
+    if (e != hipSuccess) {
+        (void)hipFree(ctx->argmax_ws);
+        (void)hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return ATLAS_ERR_COMMAND_FAILED;
     }
     *out = ctx;
     return ATLAS_OK;
@@ -823,7 +857,9 @@ static int logits_rows(atlas_hip_ctx* ctx, const float* logits, float* capped, u
     if ((reinterpret_cast<uintptr_t>(logits) | reinterpret_cast<uintptr_t>(capped) |
          reinterpret_cast<uintptr_t>(selected)) & 3)
         return invalid(ctx, "logits and selected must be 4-byte aligned");
-    return launched(ctx, atlas::launch_logits_f32(ctx->stream, logits, capped, selected, rows, count, cap, ctx->argmax_ws),
+    return launched(ctx,
+                    atlas::launch_logits_f32(ctx->stream, logits, capped, selected, rows, count, cap, ctx->argmax_ws,
+                                             atlas::kArgmaxSlots),
                     op);
 }
 
@@ -835,6 +871,31 @@ int atlas_hip_softcap_argmax_f32(atlas_hip_ctx* ctx, const float* logits, float*
                                  uint32_t rows, uint32_t count, float cap) {
     if (ctx && !finite_cap(cap)) return invalid(ctx, "logit soft cap must be finite and positive");
     return logits_rows(ctx, logits, capped, selected, rows, count, cap, "softcap_argmax_f32");
+}
+
+// The same computation with the per-workgroup partial keys in the library's
+// static scratch (this device's copy, resolved at init) instead of the
+// context's workspace: no allocation of any kind, one launch pair per call.
+int atlas_hip_softcap_argmax_f32_noalloc(atlas_hip_ctx* ctx, const float* logits, float* capped,
+                                         uint32_t* selected, uint32_t rows, uint32_t count, float cap) {
+    int rc = enter(ctx);
+    if (rc) return rc;
+    if (!finite_cap(cap)) return invalid(ctx, "logit soft cap must be finite and positive");
+    if (!logits || !selected) return invalid(ctx, "argmax buffer is null");
+    if (rows == 0 || count == 0) return invalid(ctx, "argmax requires at least one value per row");
+    if ((reinterpret_cast<uintptr_t>(logits) | reinterpret_cast<uintptr_t>(capped) |
+         reinterpret_cast<uintptr_t>(selected)) & 3)
+        return invalid(ctx, "logits and selected must be 4-byte aligned");
+    if (!ctx->argmax_scratch) return invalid(ctx, "the argmax scratch was not resolved for this device");
+    if (atlas::logits_launches(logits, capped, rows, count, atlas::kArgmaxScratchSlots) != 1)
+        return fail(ctx, ATLAS_ERR_INVALID_INPUT,
+                    "invalid buffer/input: rows x workgroups per row exceed the no-allocation argmax scratch "
+                    "(%u slots; it holds up to 256 rows of 262144 values, 64 rows of 1048576)",
+                    atlas::kArgmaxScratchSlots);
+    return launched(ctx,
+                    atlas::launch_logits_f32(ctx->stream, logits, capped, selected, rows, count, cap,
+                                             ctx->argmax_scratch, atlas::kArgmaxScratchSlots),
+                    "softcap_argmax_f32_noalloc");
 }
 
 int atlas_hip_ple_q4_0(atlas_hip_ctx* ctx, const uint8_t* table, const uint32_t* ids, const float* projection,

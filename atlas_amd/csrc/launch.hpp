@@ -148,8 +148,19 @@ size_t argmax_workspace_bytes();
 // cap > 0: capped = cap * tanh(logits / cap) (capped may alias logits or be
 // null when only the argmax is wanted); selected != null: selected[r] =
 // argmax of row r of the (capped) logits.  rows x count values, count >= 1.
+// workspace holds slot_count 64-bit slots; rows are split over as many
+// launches as that needs.
 hipError_t launch_logits_f32(hipStream_t stream, const float* logits, float* capped, uint32_t* selected,
-                             uint32_t rows, uint32_t count, float cap, void* workspace);
+                             uint32_t rows, uint32_t count, float cap, void* workspace, uint32_t slot_count);
+// Launches launch_logits_f32 makes for these operands with slot_count slots
+// (0 if a row needs more slots than that).
+uint32_t logits_launches(const float* logits, const float* capped, uint32_t rows, uint32_t count,
+                         uint32_t slot_count);
+// The library's static scratch for the no-allocation soft cap + argmax:
+// kArgmaxScratchSlots slots (128 KiB per GPU).  argmax_scratch_address gives
+// the current device's copy (hipGetSymbolAddress).
+constexpr uint32_t kArgmaxScratchSlots = 16384;
+hipError_t argmax_scratch_address(void** ptr);
 hipError_t launch_softcap_f32(hipStream_t stream, const float* in, float* out, uint64_t n, float cap);
 
 }  // namespace atlas

@@ -157,24 +157,44 @@ __global__ __launch_bounds__(kLogitThreads) void logits_scalar_kernel(const floa
     if (ARG) publish_key(key, row, slots, selected);
 }
 
-template <bool CAP, bool ARG>
-hipError_t launch_rows(hipStream_t stream, const float* in, float* out, uint32_t* selected, uint32_t rows,
-                       uint32_t count, float cap, uint64_t* slots) {
-    const bool vec = count % 4 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 &&
-                     (!out || (reinterpret_cast<uintptr_t>(out) & 15) == 0);
+// The grid of a soft cap / argmax over rows x count values: `blocks`
+// workgroups per row, each covering `per_block` values.
+struct RowSplit {
+    bool vec, wide;
+    uint32_t blocks, per_block;
+};
+
+RowSplit row_split(const float* in, const float* out, uint32_t rows, uint32_t count) {
+    RowSplit r;
+    r.vec = count % 4 == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 &&
+            (!out || (reinterpret_cast<uintptr_t>(out) & 15) == 0);
     // large batches: steps of 4096 values; a single row: 1024, for more
     // workgroups in flight.  At most kArgmaxSlotsPerRow workgroups per row:
     // longer rows give each workgroup several steps.
-    const bool wide = static_cast<uint64_t>(rows) * count >= (1u << 22);
-    const uint32_t step = vec && wide ? 4096u : 1024u;
-    uint32_t blocks = (count + step - 1) / step;
-    uint32_t per_block = step;
-    if (blocks > kArgmaxSlotsPerRow) {
-        per_block = ((count + kArgmaxSlotsPerRow - 1) / kArgmaxSlotsPerRow + step - 1) / step * step;
-        blocks = (count + per_block - 1) / per_block;
+    r.wide = static_cast<uint64_t>(rows) * count >= (1u << 22);
+    const uint32_t step = r.vec && r.wide ? 4096u : 1024u;
+    r.blocks = (count + step - 1) / step;
+    r.per_block = step;
+    if (r.blocks > kArgmaxSlotsPerRow) {
+        r.per_block = ((count + kArgmaxSlotsPerRow - 1) / kArgmaxSlotsPerRow + step - 1) / step * step;
+        r.blocks = (count + r.per_block - 1) / r.per_block;
     }
-    // one launch covers as many rows as the workspace has slots for
-    const uint32_t rows_per_launch = blocks == 1 ? 65535u : kArgmaxSlots / blocks;
+    return r;
+}
+
+// Rows one launch can cover with `slot_count` workspace slots (a row split
+// over one workgroup writes its result directly and needs none).
+uint32_t row_launch_rows(uint32_t blocks, uint32_t slot_count) {
+    return blocks == 1 ? 65535u : slot_count / blocks;
+}
+
+template <bool CAP, bool ARG>
+hipError_t launch_rows(hipStream_t stream, const float* in, float* out, uint32_t* selected, uint32_t rows,
+                       uint32_t count, float cap, uint64_t* slots, uint32_t slot_count) {
+    const RowSplit split = row_split(in, out, rows, count);
+    const bool vec = split.vec, wide = split.wide;
+    const uint32_t blocks = split.blocks, per_block = split.per_block;
+    const uint32_t rows_per_launch = row_launch_rows(blocks, slot_count);
     for (uint32_t r0 = 0; r0 < rows; r0 += rows_per_launch) {
         const uint32_t n = rows - r0 < rows_per_launch ? rows - r0 : rows_per_launch;
         const dim3 grid(blocks, n);
@@ -235,13 +255,36 @@ uint32_t grid_for(uint64_t items) {
 size_t argmax_workspace_bytes() { return kArgmaxSlots * sizeof(uint64_t); }
 
 hipError_t launch_logits_f32(hipStream_t stream, const float* logits, float* capped, uint32_t* selected,
-                             uint32_t rows, uint32_t count, float cap, void* workspace) {
+                             uint32_t rows, uint32_t count, float cap, void* workspace, uint32_t slot_count) {
     uint64_t* slots = static_cast<uint64_t*>(workspace);
     const bool do_cap = cap > 0.0f;
     if (do_cap && selected)
-        return launch_rows<true, true>(stream, logits, capped, selected, rows, count, cap, slots);
-    if (selected) return launch_rows<false, true>(stream, logits, nullptr, selected, rows, count, cap, slots);
-    return launch_rows<true, false>(stream, logits, capped, nullptr, rows, count, cap, slots);
+        return launch_rows<true, true>(stream, logits, capped, selected, rows, count, cap, slots, slot_count);
+    if (selected)
+        return launch_rows<false, true>(stream, logits, nullptr, selected, rows, count, cap, slots, slot_count);
+    return launch_rows<true, false>(stream, logits, capped, nullptr, rows, count, cap, slots, slot_count);
+}
+
+uint32_t logits_launches(const float* logits, const float* capped, uint32_t rows, uint32_t count,
+                         uint32_t slot_count) {
+    const RowSplit split = row_split(logits, capped, rows, count);
+    const uint32_t per = row_launch_rows(split.blocks, slot_count);
+    return per == 0 ? 0u : (rows + per - 1) / per;
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of the no-allocation soft cap + argmax entry point: a file-scope
+// device array, one per GPU for the life of the process.  Host code never
+// passes the symbol itself to a kernel (on the host it is only a stand-in);
+// argmax_scratch_address resolves this device's copy once, with the device
+// current, and callers pass that address.  Every slot a call reads is
+// written by the same call first, so the array needs no clearing; calls
+// that overlap on one GPU share it and race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint64_t scratch[kArgmaxScratchSlots];
+
+hipError_t argmax_scratch_address(void** ptr) {
+    return hipGetSymbolAddress(ptr, HIP_SYMBOL(scratch));
 }
 
 hipError_t launch_softcap_f32(hipStream_t stream, const float* in, float* out, uint64_t n, float cap) {

@@ -312,6 +312,11 @@ class HipRuntime:
         self._check(self.lib.atlas_hip_softcap_argmax_f32(self.ctx, _ptr(logits), _ptr(capped), _ptr(selected), rows,
                                                           count, cap))
 
+    def softcap_argmax_noalloc(self, logits, capped, selected, rows, count, cap):
+        """The no-allocation variant (static device scratch, one launch pair)."""
+        self._check(self.lib.atlas_hip_softcap_argmax_f32_noalloc(self.ctx, _ptr(logits), _ptr(capped),
+                                                                  _ptr(selected), rows, count, cap))
+
     def matmul_q4_0_gate_up_rms(self, x, gw, uw, g_out, u_out, input_width, output_width, rms_weight, eps):
         self._check(self.lib.atlas_hip_matmul_q4_0_gate_up_rms_f32(self.ctx, _ptr(x), _ptr(gw), _ptr(uw), _ptr(g_out),
                                                                    _ptr(u_out), input_width, output_width,
