@@ -100,22 +100,54 @@ class GemmaDecodeStep:
         self._upload_tables()
 
     # -- the chain ---------------------------------------------------------
-    def enqueue(self) -> None:
+    def head_ops(self):
+        """The step's two gathers, [(name, algorithmic bytes, launch)]:
+        the Q4_0 token embedding x sqrt(hidden) and the PLE chain
+        (gemma4_executor.rs:4145-4237)."""
+        rt, S, d, o = self.rt, self.S, self.dev, self.out
+        B, H, L, W = S.batch, S.hidden, S.layers, S.ple_width
+        return [
+            ("embed_q4_0", B * wl.q_row_bytes(H, False) + B * 4 + B * H * 4,
+             lambda: rt.embed_q4_0(d["token_table"], d["ids"], o["state"], self.vocab, H, B, wl.f32_sqrt(H))),
+            ("ple_q4_0", B * wl.q_row_bytes(L * W, False) + B * 4 + 2 * B * L * W * 4,
+             lambda: rt.ple_q4_0(d["ple_table"], d["ids"], d["ple_proj_in"], o["ple"], self.vocab, L, W, B, 16.0,
+                                 wl.SQRT_2_RECIP)),
+        ]
+
+    def layer_ops(self, layer: int):
+        """One layer's six fused ops in the reference decode order
+        (encode_current_token, gemma4_executor.rs:4123-4690),
+        [(name, algorithmic bytes, launch)]."""
         rt, S, d, o = self.rt, self.S, self.dev, self.out
         B, H, QH, D, F, L, W = S.batch, S.hidden, S.q_heads, S.head_dim, S.ffn, S.layers, S.ple_width
-        rt.embed_q4_0(d["token_table"], d["ids"], o["state"], self.vocab, H, B, wl.f32_sqrt(H))
-        rt.ple_q4_0(d["ple_table"], d["ids"], d["ple_proj_in"], o["ple"], self.vocab, L, W, B, 16.0,
-                    wl.SQRT_2_RECIP)
-        for layer, lay in enumerate(self.dlayers):
-            g = S.is_global(layer)
-            cos, sin = (d["cos_global"], d["sin_global"]) if g else (d["cos_local"], d["sin_local"])
-            rt.qk_norm_rope(lay["q"], lay["k"], lay["qw"], lay["kw"], cos, sin, o["q_out"][layer],
-                            o["k_out"][layer], B, QH, 1, D, D // 2, S.eps)
-            rt.rms_norm_residual(lay["attn_out"], lay["post_attn_w"], o["state"], None, o["state"], B, H, S.eps)
-            rt.geglu(lay["gate"], lay["up"], o["ffn_act"][layer], B * F)
-            rt.rms_norm_residual(lay["ffn_out"], lay["post_ffn_w"], o["state"], None, o["state"], B, H, S.eps)
-            rt.geglu_offset(lay["ple_gate"], o["ple"], o["ple_act"][layer], layer * W, L * W, W, B)
-            rt.rms_norm_add_scale(lay["ple_proj"], lay["post_norm_w"], o["state"], lay["scale"], B, H, S.eps)
+        lay = self.dlayers[layer]
+        g = S.is_global(layer)
+        cos, sin = (d["cos_global"], d["sin_global"]) if g else (d["cos_local"], d["sin_local"])
+        rms_res = 3 * B * H * 4 + H * 4
+        return [
+            ("qk_norm_rope", 2 * B * (QH + 1) * D * 4 + 2 * B * (D // 2) * 4 + 2 * D * 4,
+             lambda: rt.qk_norm_rope(lay["q"], lay["k"], lay["qw"], lay["kw"], cos, sin, o["q_out"][layer],
+                                     o["k_out"][layer], B, QH, 1, D, D // 2, S.eps)),
+            ("rms_residual_attn", rms_res,
+             lambda: rt.rms_norm_residual(lay["attn_out"], lay["post_attn_w"], o["state"], None, o["state"], B, H,
+                                          S.eps)),
+            ("geglu", 3 * B * F * 4, lambda: rt.geglu(lay["gate"], lay["up"], o["ffn_act"][layer], B * F)),
+            ("rms_residual_ffn", rms_res,
+             lambda: rt.rms_norm_residual(lay["ffn_out"], lay["post_ffn_w"], o["state"], None, o["state"], B, H,
+                                          S.eps)),
+            ("geglu_offset_ple", 3 * B * W * 4,
+             lambda: rt.geglu_offset(lay["ple_gate"], o["ple"], o["ple_act"][layer], layer * W, L * W, W, B)),
+            ("rms_add_scale_ple", 3 * B * H * 4 + H * 4 + 4,
+             lambda: rt.rms_norm_add_scale(lay["ple_proj"], lay["post_norm_w"], o["state"], lay["scale"], B, H,
+                                           S.eps)),
+        ]
+
+    def enqueue(self) -> None:
+        for _, _, launch in self.head_ops():
+            launch()
+        for layer in range(self.S.layers):
+            for _, _, launch in self.layer_ops(layer):
+                launch()
 
     def capture(self) -> int:
         """Record one step into a HIP graph (kept on the object)."""
@@ -140,21 +172,10 @@ class GemmaDecodeStep:
     # -- accounting --------------------------------------------------------
     def bytes_per_layer(self) -> int:
         """Algorithmic HBM bytes of one layer's six ops (inputs once, outputs once)."""
-        S = self.S
-        B, H, QH, D, F, W = S.batch, S.hidden, S.q_heads, S.head_dim, S.ffn, S.ple_width
-        qk = 2 * B * (QH + 1) * D * 4 + 2 * B * (D // 2) * 4 + 2 * D * 4
-        rms_res = 3 * B * H * 4 + H * 4
-        geglu = 3 * B * F * 4
-        gate = 3 * B * W * 4
-        add_scale = 3 * B * H * 4 + H * 4 + 4
-        return qk + 2 * rms_res + geglu + gate + add_scale
+        return sum(b for _, b, _ in self.layer_ops(0))
 
     def bytes_per_step(self) -> int:
-        S = self.S
-        B, H, L, W = S.batch, S.hidden, S.layers, S.ple_width
-        embed = B * wl.q_row_bytes(H, False) + B * 4 + B * H * 4
-        ple = B * wl.q_row_bytes(L * W, False) + B * 4 + 2 * B * L * W * 4
-        return embed + ple + L * self.bytes_per_layer()
+        return sum(b for _, b, _ in self.head_ops()) + self.S.layers * self.bytes_per_layer()
 
     def results(self) -> dict:
         S = self.S

@@ -30,7 +30,8 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--reduction auto|seq
        python bench.py --copy-mib 256               (a D2D copy of known size: the PMC
                                                       calibration kernel)
        python bench.py --floor-sweep                (the streaming floor alone over the ops' sizes)
-       python bench.py --decode                     (configs[4] batched decode, separate line)
+       python bench.py --decode [--batch 1]         (configs[4] batched decode, separate line; --batch 1:
+                                                      one sequence, next to the reference's per-token figures)
        python bench.py --config c1|c2|gemv|kv|logits (other op configurations, per-op lines)
 """
 import argparse
@@ -385,86 +386,124 @@ def floor_sweep(rt, iters):
                           "frac": round((ib + ob) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
 
 
-def cpu_baseline(wl, budget_s=10.0, max_threads=16):
-    """The C oracle over a token sample of the same step, single-threaded and
-    then on every host core of the box's share (at most max_threads threads,
-    each on its own token slice; ctypes releases the GIL during each C call).
-    The oracle is test infrastructure; here it is the reported CPU baseline,
-    never the product."""
+def cpu_baseline(wl, budget_s=1.0, max_threads=16, host=None):
+    """The C oracle (-O3, -ffp-contract=off; the restatement of the reference
+    CPU operators) on the same step's ops, timed on this host: each op alone
+    over 64-token slices of the full-size inputs (the 262144-row tables
+    included, so gathers read cache-cold rows), for `budget_s` seconds on one
+    thread and then `budget_s` on every host core of the box's share (at most
+    max_threads threads, each on its own token slices; ctypes releases the
+    GIL during each C call).  Per op: GB/s (algorithmic bytes) and tokens/s
+    on 1 and N cores; the step's tokens/s is 1 / the sum of the ops' seconds
+    per token.  `host`: the step's full-size inputs (Ops.host); generated
+    here when None.  The oracle is test infrastructure; here it is the
+    reported CPU baseline, never the product."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import threading
     import oracle as ora
 
     L, Q = wl.GemmaLayerShape(), wl.QuantGatherShape()
-    Ts, H, D, QH, F = 64, L.hidden, L.head_dim, L.q_heads, L.ffn
+    T, Ts, H, D, QH, F = L.tokens, 64, L.hidden, L.head_dim, L.q_heads, L.ffn
     ple_row = Q.ple_layers * Q.ple_width
-    vocab = 4096  # a gather's cost does not depend on the vocabulary size
+    vocab = Q.vocab
     scale = float(wl.f32_sqrt(H))
+    if host is None:
+        r = wl.rng(2024)
+        host = {"q4": wl.q4_0_table(r, vocab, H), "q6": wl.q6_k_table(r, vocab, H),
+                "ple": wl.q4_0_table(r, vocab, ple_row), "ids": wl.token_ids(r, T, vocab),
+                "w": wl.normal(r, H, 1.0, 0.1), "qw": wl.normal(r, D, 1.0, 0.1), "kw": wl.normal(r, D, 1.0, 0.1),
+                "x": wl.normal(r, T * H), "res": wl.normal(r, T * H), "q": wl.normal(r, T * QH * D),
+                "k": wl.normal(r, T * D), "gate": wl.normal(r, T * F), "up": wl.normal(r, T * F),
+                "proj": wl.normal(r, T * ple_row)}
+    h = host
+    cos, sin = ora.rope_tables_gemma4(np.arange(T, dtype=np.uint32), D // 2, D, L.theta_local)
 
-    def make_step(seed):
-        r = wl.rng(seed)
-        q4, q6, pt = wl.q4_0_table(r, vocab, H), wl.q6_k_table(r, vocab, H), wl.q4_0_table(r, vocab, ple_row)
-        ids = wl.token_ids(r, Ts, vocab)
-        x, res, w = wl.normal(r, Ts * H), wl.normal(r, Ts * H), wl.normal(r, H, 1, 0.1)
-        q, k = wl.normal(r, Ts * QH * D), wl.normal(r, Ts * D)
-        qw, kw = wl.normal(r, D, 1, 0.1), wl.normal(r, D, 1, 0.1)
-        c, s = ora.rope_tables_gemma4(np.arange(Ts, dtype=np.uint32), D // 2, D, L.theta_local)
-        g, u, proj = wl.normal(r, Ts * F), wl.normal(r, Ts * F), wl.normal(r, Ts * ple_row)
+    def sl(a, t0, width):
+        return a[t0 * width:(t0 + Ts) * width]
 
-        def step():
-            ora.embed_q4_0(q4, ids, vocab, H, scale)
-            ora.embed_q6_k(q6, ids, vocab, H, scale)
-            ora.ple(pt, ids, proj, vocab, Q.ple_layers, Q.ple_width, 16.0, float(wl.SQRT_2_RECIP))
-            ora.rms_norm(x, w, Ts, H, L.eps)
-            ora.qk_norm_rope(q, k, qw, kw, c, s, Ts, QH, True, D, D // 2, L.eps)
-            ora.rms_norm_residual(x, w, res, Ts, H, L.eps)
-            ora.geglu(g, u)
-        return step
+    # name: (algorithmic bytes per token, call on tokens [t0, t0 + Ts))
+    per_tok = {
+        "embed_q4_0": (wl.q_row_bytes(H, False) + 4 + H * 4,
+                       lambda t0: ora.embed_q4_0(h["q4"], h["ids"][t0:t0 + Ts], vocab, H, scale)),
+        "embed_q6_k": (wl.q_row_bytes(H, True) + 4 + H * 4,
+                       lambda t0: ora.embed_q6_k(h["q6"], h["ids"][t0:t0 + Ts], vocab, H, scale)),
+        "ple_q4_0": (wl.q_row_bytes(ple_row, False) + 4 + 2 * ple_row * 4,
+                     lambda t0: ora.ple(h["ple"], h["ids"][t0:t0 + Ts], sl(h["proj"], t0, ple_row), vocab,
+                                        Q.ple_layers, Q.ple_width, 16.0, float(wl.SQRT_2_RECIP))),
+        "rms_norm": (2 * H * 4, lambda t0: ora.rms_norm(sl(h["x"], t0, H), h["w"], Ts, H, L.eps)),
+        "qk_norm_rope": (2 * (QH + 1) * D * 4 + 2 * (D // 2) * 4,
+                         lambda t0: ora.qk_norm_rope(sl(h["q"], t0, QH * D), sl(h["k"], t0, D), h["qw"], h["kw"],
+                                                     cos[t0:t0 + Ts], sin[t0:t0 + Ts], Ts, QH, True, D, D // 2,
+                                                     L.eps)),
+        "rms_residual": (3 * H * 4, lambda t0: ora.rms_norm_residual(sl(h["x"], t0, H), h["w"], sl(h["res"], t0, H),
+                                                                      Ts, H, L.eps)),
+        "geglu": (3 * F * 4, lambda t0: ora.geglu(sl(h["gate"], t0, F), sl(h["up"], t0, F))),
+    }
 
-    def timed(steps):
-        """Each step function on its own thread until budget_s; tokens/s."""
-        reps, stop = [0] * len(steps), [0.0]
-        # the deadline starts when every thread has warmed up
-        start = threading.Barrier(len(steps) + 1, action=lambda: stop.__setitem__(0, time.perf_counter() + budget_s))
+    def run(fn, threads):
+        """Calls of fn on `threads` threads for budget_s; seconds per token."""
+        reps, stop = [0] * threads, [0.0]
+        start = threading.Barrier(threads + 1, action=lambda: stop.__setitem__(0, time.perf_counter() + budget_s))
 
         def work(i):
-            steps[i]()  # warm
+            t0 = (i * 977 * Ts) % (T - Ts)
+            fn(t0)  # warm
             start.wait()
             while time.perf_counter() < stop[0]:
-                steps[i]()
+                fn(t0)
                 reps[i] += 1
-        pool = [threading.Thread(target=work, args=(i,)) for i in range(len(steps))]
+                t0 = (t0 + 7 * Ts) % (T - Ts)
+        pool = [threading.Thread(target=work, args=(i,)) for i in range(threads)]
         for t in pool:
             t.start()
         start.wait()
-        t0 = stop[0] - budget_s
+        t_begin = stop[0] - budget_s
         for t in pool:
             t.join()
-        el = time.perf_counter() - t0
-        return Ts * sum(reps) / el, sum(reps), el
+        el = time.perf_counter() - t_begin
+        return el / (Ts * max(1, sum(reps)))
 
-    one, reps1, el1 = timed([make_step(99)])
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count() or 1
     threads = max(1, min(max_threads, cores))
-    many, reps_n, el_n = timed([make_step(99 + i) for i in range(threads)]) if threads > 1 else (one, reps1, el1)
-    return {"value": round(many, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "single_thread": round(one, 1),
-            "sample": f"the full step over {Ts}-token slices, C oracle (-O2, -ffp-contract=off), same op list "
-                      f"and per-token shapes (gather vocab 4096): {reps_n} slice passes on {threads} threads "
-                      f"({el_n:.1f} s, one slice per thread); single thread {reps1} passes ({el1:.1f} s)"}
+    ops, s1, sn = {}, 0.0, 0.0
+    for name, (bpt, fn) in per_tok.items():
+        one = run(fn, 1)
+        many = run(fn, threads) if threads > 1 else one
+        s1, sn = s1 + one, sn + many
+        ops[name] = {"GB/s_1core": round(bpt / one / 1e9, 3), f"GB/s_{threads}cores": round(bpt / many / 1e9, 3),
+                     "tokens_per_s_1core": round(1.0 / one, 1), f"tokens_per_s_{threads}cores": round(1.0 / many, 1)}
+    return {"value": round(1.0 / sn, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "single_thread": round(1.0 / s1, 1), "ops": ops,
+            "sample": f"each op of the step alone over 64-token slices of the full-size inputs (262144-row "
+                      f"tables), the C oracle built -O3 -ffp-contract=off: {budget_s:g} s on 1 thread and "
+                      f"{budget_s:g} s on {threads} threads per op; step tokens/s = 1 / sum of the ops' "
+                      f"seconds per token"}
 
 
-def decode_bench(rt, steps, warmup):
-    """256 sequences x 1 token, 35 layers of the fused ops in
-    the reference decode order (atlas_amd.decode), eager and as one HIP graph."""
+# The reference's published decode figures for this path (Apple M2 Max, one
+# sequence, whole model; BASELINE.md section 1): context only, not comparable
+# hardware or batch.
+M2_MAX_CONTEXT = {
+    "qk_norm_rope_ms_per_token": 2.31,      # docs/atlas-metal-phases/next-improvements.md:51-56
+    "ple_family_ms_per_token": 1.7,         # docs/atlas-metal-phases/README.md:51-54
+    "decode_gpu_ms_per_token": 18.8,        # docs/atlas-metal-phases/README.md:51
+}
+
+
+def decode_bench(rt, steps, warmup, batch=256):
+    """`batch` sequences x 1 token (256 by default; 1 for
+    the single-sequence decode the reference publishes), 35 layers of the
+    fused ops in the reference decode order (atlas_amd.decode), eager and as
+    one HIP graph; then each op alone, timed as a graph of its 35 per-layer
+    launches (the whole step's dispatch mode)."""
     from atlas_amd import workloads as wl
     from atlas_amd.decode import GemmaDecodeStep
 
-    S = wl.DecodeShape()
-    log("building the decode step (35 layers of seeded weights and stand-ins)")
+    S = wl.DecodeShape(batch=batch)
+    log(f"building the decode step ({batch} sequences, 35 layers of seeded weights and stand-ins)")
     step = GemmaDecodeStep(rt, S, seed=5)
 
     def timed(fn, n):
@@ -482,26 +521,58 @@ def decode_bench(rt, steps, warmup):
     eager_us = timed(step.enqueue, steps)
     step.capture()
     graph_us = timed(step.replay, steps)
-    d, o, H, L, W = step.dev, step.out, S.hidden, S.layers, S.ple_width
 
-    def head():
-        rt.embed_q4_0(d["token_table"], d["ids"], o["state"], step.vocab, H, S.batch, wl.f32_sqrt(H))
-        rt.ple_q4_0(d["ple_table"], d["ids"], d["ple_proj_in"], o["ple"], step.vocab, L, W, S.batch, 16.0,
-                    wl.SQRT_2_RECIP)
+    def graph_of(calls):
+        rt.graph_begin()
+        try:
+            for c in calls:
+                c()
+        finally:
+            g = rt.graph_end()
+        return g
 
-    head_us = timed(head, steps)
+    L = S.layers
+    per_op = {}
+    heads = step.head_ops()
+    for i, (name, nbytes, _) in enumerate(heads):
+        g = graph_of([heads[i][2]] * L)
+        us = timed(lambda: rt.graph_launch(g), steps) / L
+        rt.graph_destroy(g)
+        per_op[name] = {"us": round(us, 3), "bytes": nbytes, "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "per": "step"}
+    layer_ops = [step.layer_ops(layer) for layer in range(L)]
+    for k, (name, nbytes, _) in enumerate(layer_ops[0]):
+        g = graph_of([ops[k][2] for ops in layer_ops])
+        us = timed(lambda: rt.graph_launch(g), steps) / L
+        rt.graph_destroy(g)
+        per_op[name] = {"us": round(us, 3), "bytes": nbytes, "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "per": "layer"}
+    head_us = sum(v["us"] for v in per_op.values() if v["per"] == "step")
     step.close()
     per_layer = (graph_us - head_us) / L
-    return {"metric": "C5 batched decode: per-layer latency of the fused ops (graph replay), 1 GPU",
-            "value": round(per_layer, 3), "unit": "us/layer", "higher_is_better": False, "n_gpus": 1,
-            "steps": steps, "warmup": warmup, "dtype": "f32", "data": "synthetic",
-            "config": {"workload": "gemma4-e2b-batched-decode (configs[4])", "sequences": S.batch,
-                       "layers": L, "hidden": H, "ffn": S.ffn, "q_heads": S.q_heads, "head_dim": S.head_dim,
-                       "theta": "1e4 local / 1e6 global, 4:1", "ops_per_layer": 6},
-            "step_us_graph": round(graph_us, 2), "step_us_eager": round(eager_us, 2),
-            "embed_ple_us": round(head_us, 2), "bytes_per_layer": step.bytes_per_layer(),
-            "layer_GB/s": round(step.bytes_per_layer() / (per_layer * 1e-6) / 1e9, 1),
-            "step_GB/s": round(step.bytes_per_step() / (graph_us * 1e-6) / 1e9, 1)}
+    result = {"metric": f"C5 decode ({batch} sequence{'s' if batch > 1 else ''}): per-layer latency of the fused "
+                        f"ops (graph replay), 1 GPU",
+              "value": round(per_layer, 3), "unit": "us/layer", "higher_is_better": False, "n_gpus": 1,
+              "steps": steps, "warmup": warmup, "dtype": "f32", "data": "synthetic",
+              "config": {"workload": "gemma4-e2b-batched-decode (configs[4])", "sequences": batch,
+                         "layers": L, "hidden": S.hidden, "ffn": S.ffn, "q_heads": S.q_heads,
+                         "head_dim": S.head_dim, "vocab": S.vocab, "theta": "1e4 local / 1e6 global, 4:1",
+                         "ops_per_layer": 6},
+              "step_us_graph": round(graph_us, 2), "step_us_eager": round(eager_us, 2),
+              "embed_ple_us": round(head_us, 2), "bytes_per_layer": step.bytes_per_layer(),
+              "layer_GB/s": round(step.bytes_per_layer() / (per_layer * 1e-6) / 1e9, 1),
+              "step_GB/s": round(step.bytes_per_step() / (graph_us * 1e-6) / 1e9, 1),
+              "per_op_us": per_op}
+    if batch == 1:
+        # per-token totals of this build next to the reference's published
+        # per-token figures (other hardware, whole model: context only)
+        result["per_token_ms"] = {
+            "qk_norm_rope_35_layers": round(per_op["qk_norm_rope"]["us"] * L / 1e3, 4),
+            "ple_family": round((per_op["ple_q4_0"]["us"] + L * (per_op["geglu_offset_ple"]["us"] +
+                                                                 per_op["rms_add_scale_ple"]["us"])) / 1e3, 4),
+            "fused_ops_step_graph": round(graph_us / 1e3, 4)}
+        result["reference_m2_max_context"] = M2_MAX_CONTEXT
+    return result
 
 
 def pmc_traffic(kernel_op):
@@ -530,7 +601,7 @@ def main():
     ap.add_argument("--reduction", choices=["auto", "sequential", "wide"], default="auto",
                     help="row-sum order: auto (the library default: tree where the output is a plain scaled row, "
                          "sequential where an epilogue cancels), sequential (bit-identical everywhere), wide")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=1.0, help="CPU baseline: seconds per op and thread count")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-floor", action="store_true",
                     help="skip the size-matched streaming floor per op")
@@ -544,6 +615,9 @@ def main():
                          "logits: the soft cap + argmax decode tail -- instead of the headline")
     ap.add_argument("--decode", action="store_true",
                     help="BASELINE configs[4] batched decode (per-layer latency, eager and HIP graph) instead")
+    ap.add_argument("--batch", type=int, default=256,
+                    help="--decode: sequences per step (256 = configs[4]; 1 = the single-sequence decode the "
+                         "reference publishes per-token figures for)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every op of this path is row-independent and this build "
@@ -563,7 +637,7 @@ def main():
         return
     floor = None if args.no_floor else StreamFloor(rt)
     if args.decode:
-        print(json.dumps(decode_bench(rt, min(args.steps, 50), min(args.warmup, 5))))
+        print(json.dumps(decode_bench(rt, min(args.steps, 50), min(args.warmup, 5), args.batch)))
         rt.close()
         return
     if args.config != "c3c4":
@@ -677,7 +751,7 @@ def main():
     }
     if not args.no_cpu:
         log("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds, host=ops.host)
     print(json.dumps(result))
     rt.close()
 

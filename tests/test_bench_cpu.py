@@ -11,13 +11,29 @@ from atlas_amd import workloads as wl  # noqa: E402
 
 
 def test_cpu_baseline_fields_single_and_threaded():
-    out = bench.cpu_baseline(wl, budget_s=0.3, max_threads=2)
-    assert set(out) >= {"value", "unit", "cores", "kind", "sample", "single_thread"}
+    """On small inputs (the field layout does not depend on the sizes)."""
+    import numpy as np
+    L, Q = wl.GemmaLayerShape(), wl.QuantGatherShape()
+    T, H, D, QH, F = L.tokens, L.hidden, L.head_dim, L.q_heads, L.ffn
+    r = wl.rng(1)
+    ple_row = Q.ple_layers * Q.ple_width
+    vocab = Q.vocab
+    # full-vocabulary tables are large; a table of 512 rows with ids below 512 exercises the same calls
+    host = {"q4": wl.q4_0_table(r, 512, H), "q6": wl.q6_k_table(r, 512, H), "ple": wl.q4_0_table(r, 512, ple_row),
+            "ids": wl.token_ids(r, T, 512), "w": wl.normal(r, H, 1.0, 0.1), "qw": wl.normal(r, D, 1.0, 0.1),
+            "kw": wl.normal(r, D, 1.0, 0.1), "x": wl.normal(r, T * H), "res": wl.normal(r, T * H),
+            "q": wl.normal(r, T * QH * D), "k": wl.normal(r, T * D), "gate": wl.normal(r, T * F),
+            "up": wl.normal(r, T * F), "proj": wl.normal(r, T * ple_row)}
+    assert vocab >= 512 and host["ids"].max() < 512
+    out = bench.cpu_baseline(wl, budget_s=0.05, max_threads=2, host=host)
+    assert set(out) >= {"value", "unit", "cores", "kind", "sample", "single_thread", "ops"}
     assert out["unit"] == "tokens/s" and out["kind"] == "port"
     assert 1 <= out["cores"] <= 2
     assert out["value"] > 0 and out["single_thread"] > 0
-    if out["cores"] == 1:
-        assert out["value"] == out["single_thread"]
+    assert set(out["ops"]) == {"embed_q4_0", "embed_q6_k", "ple_q4_0", "rms_norm", "qk_norm_rope", "rms_residual",
+                               "geglu"}
+    for op in out["ops"].values():
+        assert op["GB/s_1core"] > 0 and np.isfinite(op["tokens_per_s_1core"])
 
 
 def test_stream_floor_library_exports():
