@@ -303,9 +303,10 @@ hipError_t launch_embed_quant_cfg(hipStream_t stream, const uint8_t* table, cons
 template <int FMT>
 hipError_t launch_embed_fmt(hipStream_t stream, const uint8_t* table, const uint32_t* ids, float* out,
                             uint32_t vocab, uint32_t hidden, uint32_t tokens, float scale) {
-    // a wavefront per workgroup when four rows would not fit 64 KiB of LDS
-    // (hidden up to 65536: one Q6_K row is 53760 bytes)
-    const bool four = 4u * ((quant_row_bytes(FMT, hidden) + 15) & ~15u) <= 65536u;
+    // a wavefront per workgroup for decode batches (so 256 tokens spread over
+    // 256 CUs) and when four rows would not fit 64 KiB of LDS (hidden up to
+    // 65536: one Q6_K row is 53760 bytes)
+    const bool four = tokens >= 2048 && 4u * ((quant_row_bytes(FMT, hidden) + 15) & ~15u) <= 65536u;
     return four ? launch_embed_quant_cfg<FMT, 1, 4>(stream, table, ids, out, vocab, hidden, tokens, scale)
                 : launch_embed_quant_cfg<FMT, 1, 1>(stream, table, ids, out, vocab, hidden, tokens, scale);
 }

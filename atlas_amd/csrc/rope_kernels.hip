@@ -374,15 +374,20 @@ hipError_t launch_qk_token_cfg(hipStream_t s, const float* q, const float* k, co
     return hipErrorInvalidValue;
 }
 
-// One token per wavefront, four wavefronts per workgroup.  Measured on
-// MI355X at C3 (4096 tokens, 8 Q heads + K, head_dim 256): 14.17 us against
-// 14.25-14.33 with one wavefront per workgroup and 14.9-15.0 with two tokens
-// per wavefront (their two folds then share one wavefront's critical path).
+// One token per wavefront; four wavefronts per workgroup from 2048 tokens
+// up.  Measured on MI355X at C3 (4096 tokens, 8 Q heads + K, head_dim 256):
+// 14.17 us against 14.25-14.33 with one wavefront per workgroup and 14.9-15.0
+// with two tokens per wavefront (their two folds then share one wavefront's
+// critical path).  Decode batches keep one wavefront per workgroup, so 256
+// tokens still spread over 256 CUs.
 template <int P>
 hipError_t launch_qk_token_p(hipStream_t s, const float* q, const float* k, const float* qw, const float* kw,
                              const float* c, const float* sn, float* qo, float* ko, uint32_t tokens,
                              uint32_t q_heads, uint32_t has_key, uint32_t rope_stride, float eps) {
-    return launch_qk_token_cfg<P, 1, 4>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
+    if (tokens >= 2048)
+        return launch_qk_token_cfg<P, 1, 4>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride,
+                                            eps);
+    return launch_qk_token_cfg<P, 1, 1>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
 }
 
 // Generic head_dim fallback (even head_dim not of the form 64*V): one wave

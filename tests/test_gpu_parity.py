@@ -170,8 +170,10 @@ def test_reference_fusion_parity_seeds(rt, ora):
 @pytest.mark.parametrize("head_dim,rope_stride,q_heads,has_key", [
     (256, 128, 8, True), (256, 256, 8, True), (512, 256, 8, True), (128, 64, 4, True), (256, 128, 8, False),
     (96, 48, 3, True), (64, 32, 2, True)])
-def test_qk_norm_rope_shapes(rt, ora, head_dim, rope_stride, q_heads, has_key):
-    inp, m = cases.qk_case(37, q_heads, head_dim, rope_stride, 1e6, 1e-6, 500 + head_dim, has_key, start=1000)
+@pytest.mark.parametrize("tokens", [37, 2051])
+def test_qk_norm_rope_shapes(rt, ora, head_dim, rope_stride, q_heads, has_key, tokens):
+    """One and four wavefronts per workgroup (2051 tokens: a ragged last workgroup)."""
+    inp, m = cases.qk_case(tokens, q_heads, head_dim, rope_stride, 1e6, 1e-6, 500 + head_dim, has_key, start=1000)
     tables = rope_tables_gemma4(inp["pos"], rope_stride, head_dim, 1e6)
     say(f"qk_norm_rope {m}")
     assert_bits("qk", cases.qk_gpu(rt, inp, m, tables), cases.qk_oracle(ora, inp, m))
@@ -280,7 +282,7 @@ def test_full_size_gathers_c4(rt, ora):
 
 
 @pytest.mark.parametrize("fmt", ["q4_0", "q6_k", "q8_0"])
-@pytest.mark.parametrize("hidden,tokens", [(256, 1), (1536, 4097), (2048, 3), (8960, 65), (19968, 9), (20224, 9),
+@pytest.mark.parametrize("hidden,tokens", [(256, 1), (1536, 4097), (2048, 3), (8960, 65), (19968, 9), (20224, 9), (20224, 2049),
                                            (28672, 5), (29184, 5), (65536, 3)])
 def test_embed_quant_shapes(rt, ora, fmt, hidden, tokens):
     """Every packed gather format over row widths that keep four rows per
