@@ -231,7 +231,22 @@ __device__ __forceinline__ void stg_nt(float* p, f32x4 v) {
     __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
 }
 
-template <int J, int MODE>
+// 128-bit store of float4 column `c` of a row whose base address is
+// wavefront-uniform: POL < 0 a nontemporal global store, otherwise a buffer
+// store with that cache policy (gfx950 bits: sc0 = 1, nt = 2, sc1 = 16)
+// through a resource covering the row's `bytes`.
+template <int POL>
+__device__ __forceinline__ void st_row(float* row, uint32_t bytes, uint32_t c, f32x4 v) {
+    if constexpr (POL < 0) {
+        stg_nt(row + 4 * c, v);
+    } else {
+        typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+        const auto rs = __builtin_amdgcn_make_buffer_rsrc(row, 0, bytes, 0x00020000);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rs, 16u * c, 0, POL);
+    }
+}
+
+template <int J, int MODE, int POL = -1>
 struct TreeRow {
     static constexpr bool kOperand = MODE != kNormPlain;
     f32x4 x[J];
@@ -245,6 +260,20 @@ struct TreeRow {
             const uint32_t c = min(lane + 64u * j, nv - 1);
             x[j] = ldg_nt(a.x + base + 4 * c);
             if (kOperand) e[j] = ldg_nt(operand + base + 4 * c);
+        }
+    }
+
+    __device__ __forceinline__ void load_x(const NormArgs& a, uint32_t row, uint32_t lane, uint32_t nv) {
+        const size_t base = static_cast<size_t>(row) * a.hidden;
+#pragma unroll
+        for (int j = 0; j < J; ++j) x[j] = ldg_nt(a.x + base + 4 * min(lane + 64u * j, nv - 1));
+    }
+    __device__ __forceinline__ void load_e(const NormArgs& a, const float* operand, uint32_t row, uint32_t lane,
+                                           uint32_t nv) {
+        const size_t base = static_cast<size_t>(row) * a.hidden;
+        if (kOperand) {
+#pragma unroll
+            for (int j = 0; j < J; ++j) e[j] = ldg_nt(operand + base + 4 * min(lane + 64u * j, nv - 1));
         }
     }
 
@@ -266,32 +295,32 @@ struct TreeRow {
             p = p + (lane + 64u * j < nv ? q : 0.0f);
         }
         const float inv = inverse_rms(wave_sum_tree_f32(p), static_cast<float>(a.hidden), a.epsilon);
+        const uint32_t rb = a.hidden * 4u;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const uint32_t c = lane + 64u * j;
             if (c >= nv) continue;
-            const size_t idx = base + 4 * c;
             const f32x4 v = x[j], ww = w[j];
             const f32x4 n{v.x * inv * ww.x, v.y * inv * ww.y, v.z * inv * ww.z, v.w * inv * ww.w};
             if (MODE == kNormPlain) {
-                stg_nt(a.out + idx, n);
+                st_row<POL>(a.out + base, rb, c, n);
             } else if (MODE == kNormAddNorm) {
-                stg_nt(a.residual_out + idx, v);
-                stg_nt(a.out + idx, n);
+                st_row<POL>(a.residual_out + base, rb, c, v);
+                st_row<POL>(a.out + base, rb, c, n);
             } else if (MODE == kNormResidual) {
-                if (a.normalized) stg_nt(a.normalized + idx, n);
+                if (a.normalized) st_row<POL>(a.normalized + base, rb, c, n);
                 const f32x4 b = e[j];
-                stg_nt(a.out + idx, f32x4{b.x + n.x, b.y + n.y, b.z + n.z, b.w + n.w});
+                st_row<POL>(a.out + base, rb, c, f32x4{b.x + n.x, b.y + n.y, b.z + n.z, b.w + n.w});
             } else {
                 const f32x4 b = e[j];
-                stg_nt(a.out + idx,
-                       f32x4{(b.x + n.x) * scale, (b.y + n.y) * scale, (b.z + n.z) * scale, (b.w + n.w) * scale});
+                st_row<POL>(a.out + base, rb, c,
+                            f32x4{(b.x + n.x) * scale, (b.y + n.y) * scale, (b.z + n.z) * scale, (b.w + n.w) * scale});
             }
         }
     }
 };
 
-template <int J, int MODE, bool PAIR>
+template <int J, int MODE, bool PAIR, bool DEFER = false, int POL = -1>
 __global__ __launch_bounds__(256) void rms_tree_kernel(NormArgs a) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
@@ -301,9 +330,16 @@ __global__ __launch_bounds__(256) void rms_tree_kernel(NormArgs a) {
     const bool second = PAIR && r1 < a.rows;
     const uint32_t nv = a.hidden >> 2;
     const float* operand = MODE == kNormAddScale ? a.out : a.residual;
-    TreeRow<J, MODE> row0, row1;
-    row0.load(a, operand, r0, lane, nv);
-    if (second) row1.load(a, operand, r1, lane, nv);
+    TreeRow<J, MODE, POL> row0, row1;
+    if constexpr (DEFER) {
+        row0.load_x(a, r0, lane, nv);
+        if (second) row1.load_x(a, r1, lane, nv);
+        row0.load_e(a, operand, r0, lane, nv);
+        if (second) row1.load_e(a, operand, r1, lane, nv);
+    } else {
+        row0.load(a, operand, r0, lane, nv);
+        if (second) row1.load(a, operand, r1, lane, nv);
+    }
     f32x4 w[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) w[j] = ldg(a.weight + 4 * min(lane + 64u * j, nv - 1));
@@ -343,7 +379,7 @@ struct FoldScansLds {
     uint32_t e0;
 };
 
-template <int R, int J, int MODE, bool PAR, bool STAGE, bool RUN, bool STRIDED = false>
+template <int R, int J, int MODE, bool PAR, bool STAGE, bool RUN, int POL = -1>
 __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
     // Squares of R rows, (hidden/4 + 1) float4 per row.  The load phase is
     // straight-line code (rows past the end and columns past the row width
@@ -360,12 +396,9 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
     const uint32_t nv = h >> 2;
     // RUN: a row's squares at their columns, zero-padded to 64 * J float4
     const uint32_t stride4 = kRun ? 64u * J + 1 : nv + 1;
-    // the wavefront's rows: R consecutive rows, or (STRIDED) rows
-    // blockIdx.x + r * gridDim.x; either way the valid ones are r < nrows
-    const uint32_t row0 = STRIDED ? blockIdx.x : blockIdx.x * R;
-    const uint32_t row_step = STRIDED ? gridDim.x : 1u;
-    const uint32_t nrows = STRIDED ? min(static_cast<uint32_t>(R), (a.rows - row0 + row_step - 1) / row_step)
-                                   : min(static_cast<uint32_t>(R), a.rows - row0);
+    // the wavefront's R consecutive rows; the valid ones are r < nrows
+    const uint32_t row0 = blockIdx.x * R;
+    const uint32_t nrows = min(static_cast<uint32_t>(R), a.rows - row0);
     // second operand: residual (kNormResidual, kNormAddNorm) or state (kNormAddScale)
     const float* operand = MODE == kNormAddScale ? a.out : a.residual;
     FoldScansLds<4>* scans_lds = reinterpret_cast<FoldScansLds<4>*>(sq4 + stride4);
@@ -413,7 +446,7 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
         const uint32_t c = min(lane + 64u * j, nv - 1) + zero;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const size_t idx = static_cast<size_t>(row0 + min(static_cast<uint32_t>(r), nrows - 1) * row_step) * h + 4 * c;
+            const size_t idx = static_cast<size_t>(row0 + min(static_cast<uint32_t>(r), nrows - 1)) * h + 4 * c;
             x[r][j] = ldg_nt(a.x + idx);
             if (kOperand) e[r][j] = ldg_nt(operand + idx);
         }
@@ -508,7 +541,7 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
 #pragma unroll
             for (int j = 0; j < J; ++j) {
                 const uint32_t c = lane + 64u * j;
-                if (c < nv) stg_nt(a.residual_out + static_cast<size_t>(row0 + r * row_step) * h + 4 * c, x[r][j]);
+                if (c < nv) stg_nt(a.residual_out + static_cast<size_t>(row0 + r) * h + 4 * c, x[r][j]);
             }
         }
     }
@@ -520,23 +553,23 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
         if (static_cast<uint32_t>(r) >= nrows) break;
         const float ir = PAR ? inverse_rms(__uint_as_float(sb[r]), static_cast<float>(h), a.epsilon)
                              : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
+        const size_t base = static_cast<size_t>(row0 + r) * h;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const uint32_t c = lane + 64u * j;
             if (c >= nv) continue;
-            const size_t idx = static_cast<size_t>(row0 + r * row_step) * h + 4 * c;
             const f32x4 v = x[r][j], ww = w[j];
             const f32x4 n{v.x * ir * ww.x, v.y * ir * ww.y, v.z * ir * ww.z, v.w * ir * ww.w};
             if (MODE == kNormPlain || MODE == kNormAddNorm) {
-                stg_nt(a.out + idx, n);
+                st_row<POL>(a.out + base, h * 4u, c, n);
             } else if (MODE == kNormResidual) {
-                if (a.normalized) stg_nt(a.normalized + idx, n);
+                if (a.normalized) st_row<POL>(a.normalized + base, h * 4u, c, n);
                 const f32x4 b = e[r][j];
-                stg_nt(a.out + idx, f32x4{b.x + n.x, b.y + n.y, b.z + n.z, b.w + n.w});
+                st_row<POL>(a.out + base, h * 4u, c, f32x4{b.x + n.x, b.y + n.y, b.z + n.z, b.w + n.w});
             } else {
                 const f32x4 b = e[r][j];
-                stg_nt(a.out + idx,
-                       f32x4{(b.x + n.x) * scale, (b.y + n.y) * scale, (b.z + n.z) * scale, (b.w + n.w) * scale});
+                st_row<POL>(a.out + base, h * 4u, c,
+                            f32x4{(b.x + n.x) * scale, (b.y + n.y) * scale, (b.z + n.z) * scale, (b.w + n.w) * scale});
             }
         }
     }
@@ -624,15 +657,24 @@ hipError_t launch_reg(hipStream_t s, const NormArgs& a) {
 // fill the chip when each takes two).
 bool tree_pairs(uint32_t rows) { return rows >= 4096; }
 
+// The residual and add-scale epilogues need their operand only after the
+// sum: it is requested after both rows' x (DEFER).  Measured on MI355X at
+// [4096, 1536] (residual, ATLAS_REDUCTION_WIDE): 12.98-13.03 us against
+// 13.63-13.64 with x and the operand requested row by row.  Stores are
+// nontemporal buffer stores through a per-row resource (policy 2): at
+// [4096, 1536] plain 8.57-8.58 us against 8.61-8.66 with global nontemporal
+// stores; the sc1 and sc1 + nt store policies were slower (9.46, 9.19).
 template <int J, int MODE>
 hipError_t launch_tree_j(hipStream_t s, const NormArgs& a) {
+    constexpr bool kDefer = MODE == kNormResidual || MODE == kNormAddScale;
+    constexpr int kStorePolicy = 2;
     const bool pair = tree_pairs(a.rows);
     const uint32_t waves = pair ? (a.rows + 1) / 2 : a.rows;
     const dim3 grid((waves + 3) / 4);
     if (pair)
-        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, true>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, true, kDefer, kStorePolicy>), grid, dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, false>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, false, kDefer, kStorePolicy>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -101,4 +101,45 @@ int atlas_floor_stream_kind(void* stream, const void* in, size_t in_bytes, void*
     return static_cast<int>(hipGetLastError());
 }
 
+// The cache-policy sweep behind the three shapes above: the same kernel
+// with load policy `lp` and store policy `sp` (indices into kPolicies:
+// plain, nt, sc1, sc1+nt, sc0+sc1+nt) over `grid` workgroups of 256 threads
+// (0: one thread per float4 of the longer stream).
+int atlas_floor_policy_count(void) { return 5; }
+
+int atlas_floor_stream_policy(void* stream, const void* in, size_t in_bytes, void* out, size_t out_bytes,
+                              uint32_t* sink, int lp, int sp, uint32_t grid) {
+    if (lp < 0 || lp > 4 || sp < 0 || sp > 4 || in_bytes >= (1ull << 32) || out_bytes >= (1ull << 32))
+        return static_cast<int>(hipErrorInvalidValue);
+    const uint32_t in4 = static_cast<uint32_t>(in_bytes / 16), out4 = static_cast<uint32_t>(out_bytes / 16);
+    const uint32_t n4 = in4 > out4 ? in4 : out4;
+    if (n4 == 0) return 0;
+    const uint32_t full = (n4 + kThreads - 1) / kThreads;
+    const dim3 g(grid == 0 || grid > full ? full : grid);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    // kPolicies: 0 plain, 2 nt, 16 sc1, 18 sc1+nt, 19 sc0+sc1+nt
+#define ATLAS_FLOOR_SP(LP, SPV)                                                                               \
+    hipLaunchKernelGGL((stream_floor_kernel<LP, SPV>), g, dim3(kThreads), 0, s, in, in4, out, out4, sink); \
+    break;
+#define ATLAS_FLOOR_LP(LP)                  \
+    switch (sp) {                           \
+        case 0: ATLAS_FLOOR_SP(LP, 0)       \
+        case 1: ATLAS_FLOOR_SP(LP, 2)       \
+        case 2: ATLAS_FLOOR_SP(LP, 16)      \
+        case 3: ATLAS_FLOOR_SP(LP, 18)      \
+        default: ATLAS_FLOOR_SP(LP, 19)     \
+    }                                       \
+    break;
+    switch (lp) {
+        case 0: ATLAS_FLOOR_LP(0)
+        case 1: ATLAS_FLOOR_LP(2)
+        case 2: ATLAS_FLOOR_LP(16)
+        case 3: ATLAS_FLOOR_LP(18)
+        default: ATLAS_FLOOR_LP(19)
+    }
+#undef ATLAS_FLOOR_LP
+#undef ATLAS_FLOOR_SP
+    return static_cast<int>(hipGetLastError());
+}
+
 }  // extern "C"

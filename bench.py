@@ -30,6 +30,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--reduction auto|seq
        python bench.py --copy-mib 256               (a D2D copy of known size: the PMC
                                                       calibration kernel)
        python bench.py --floor-sweep                (the streaming floor alone over the ops' sizes)
+       python bench.py --policy-sweep --op-iters 100 (the floor kernel over cache policies and grid shapes)
        python bench.py --decode [--batch 1]         (configs[4] batched decode, separate line; --batch 1:
                                                       one sequence, next to the reference's per-token figures)
        python bench.py --config c1|c2|gemv|kv|logits (other op configurations, per-op lines)
@@ -360,6 +361,57 @@ class StreamFloor:
         return rt.elapsed_ms(a, b) / iters * 1e3
 
 
+POLICY_NAMES = ["plain", "nt", "sc1", "sc1+nt", "sc0+sc1+nt"]
+
+
+def policy_sweep(rt, iters):
+    """The streaming kernel over every load x store cache policy and two grid
+    shapes at the ops' sizes (one JSON line per size): the evidence for the
+    floor's three shapes."""
+    import ctypes
+
+    floor = StreamFloor(rt)
+    lib = floor.lib
+    lib.atlas_floor_stream_policy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                              ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_uint32]
+    lib.atlas_floor_stream_policy.restype = ctypes.c_int
+    sizes = [("rms", 25.2, 25.2), ("gather", 3.5, 25.2), ("residual", 50.3, 25.2), ("qk", 42.0, 37.7),
+             ("geglu", 201.3, 100.7)]
+    for name, r_mb, w_mb in sizes:
+        ib, ob = int(r_mb * 1e6) // 256 * 256, int(w_mb * 1e6) // 256 * 256
+        per_set = ib + ob
+        nsets = max(4, math.ceil(ROTATION_BYTES / per_set))
+        pool = rt.alloc(nsets * per_set)
+        rt.memset(pool, 0, nsets * per_set)
+        res = {}
+        for grid in (0, 4096):
+            for lp in range(lib.atlas_floor_policy_count()):
+                for sp in range(lib.atlas_floor_policy_count()):
+                    def launch(i):
+                        base = pool.ptr + (i % nsets) * per_set
+                        rc = lib.atlas_floor_stream_policy(floor.stream, base, ib, base + ib, ob, floor.sink.ptr, lp,
+                                                           sp, grid)
+                        if rc != 0:
+                            raise RuntimeError(f"policy sweep launch failed: HIP error {rc}")
+                    for i in range(3):
+                        launch(i)
+                    rt.sync()
+                    a, b = rt.event(), rt.event()
+                    rt.record(a)
+                    for i in range(iters):
+                        launch(i)
+                    rt.record(b)
+                    rt.sync()
+                    res[f"{'full' if grid == 0 else grid}/{POLICY_NAMES[lp]}/{POLICY_NAMES[sp]}"] = round(
+                        rt.elapsed_ms(a, b) / iters * 1e3, 3)
+        rt.free(pool)
+        best = min(res, key=res.get)
+        print(json.dumps({"size": name, "read_MB": r_mb, "write_MB": w_mb, "best": best, "best_us": res[best],
+                          "best_frac": round((ib + ob) / (res[best] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                          "us": res}), flush=True)
+
+
 def floor_fields(floor, nbytes, out_bytes, op_us, iters):
     """floor_us: the size-matched streaming floor; of_floor = floor_us / op_us
     (1.0 = the op moves its bytes as fast as a plain stream of the same size)."""
@@ -493,7 +545,7 @@ M2_MAX_CONTEXT = {
 }
 
 
-def decode_bench(rt, steps, warmup, batch=256):
+def decode_bench(rt, steps, warmup, batch=256, graphs=True):
     """`batch` sequences x 1 token (256 by default; 1 for
     the single-sequence decode the reference publishes), 35 layers of the
     fused ops in the reference decode order (atlas_amd.decode), eager and as
@@ -519,39 +571,45 @@ def decode_bench(rt, steps, warmup, batch=256):
         return rt.elapsed_ms(a, b) * 1e3 / n
 
     eager_us = timed(step.enqueue, steps)
-    step.capture()
-    graph_us = timed(step.replay, steps)
+    if graphs:
+        step.capture()
+        graph_us = timed(step.replay, steps)
+    else:
+        graph_us = eager_us
 
-    def graph_of(calls):
+    def per_launch_us(calls):
+        """Microseconds per call of `calls` run back to back: as one graph
+        (the step's dispatch mode), or eagerly with graphs off."""
+        if not graphs:
+            return timed(lambda: [c() for c in calls], steps) / len(calls)
         rt.graph_begin()
         try:
             for c in calls:
                 c()
         finally:
             g = rt.graph_end()
-        return g
+        us = timed(lambda: rt.graph_launch(g), steps) / len(calls)
+        rt.graph_destroy(g)
+        return us
 
     L = S.layers
     per_op = {}
     heads = step.head_ops()
     for i, (name, nbytes, _) in enumerate(heads):
-        g = graph_of([heads[i][2]] * L)
-        us = timed(lambda: rt.graph_launch(g), steps) / L
-        rt.graph_destroy(g)
+        us = per_launch_us([heads[i][2]] * L)
         per_op[name] = {"us": round(us, 3), "bytes": nbytes, "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
                         "per": "step"}
     layer_ops = [step.layer_ops(layer) for layer in range(L)]
     for k, (name, nbytes, _) in enumerate(layer_ops[0]):
-        g = graph_of([ops[k][2] for ops in layer_ops])
-        us = timed(lambda: rt.graph_launch(g), steps) / L
-        rt.graph_destroy(g)
+        us = per_launch_us([ops[k][2] for ops in layer_ops])
         per_op[name] = {"us": round(us, 3), "bytes": nbytes, "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
                         "per": "layer"}
     head_us = sum(v["us"] for v in per_op.values() if v["per"] == "step")
     step.close()
     per_layer = (graph_us - head_us) / L
+    mode = "graph replay" if graphs else "eager launches"
     result = {"metric": f"C5 decode ({batch} sequence{'s' if batch > 1 else ''}): per-layer latency of the fused "
-                        f"ops (graph replay), 1 GPU",
+                        f"ops ({mode}), 1 GPU",
               "value": round(per_layer, 3), "unit": "us/layer", "higher_is_better": False, "n_gpus": 1,
               "steps": steps, "warmup": warmup, "dtype": "f32", "data": "synthetic",
               "config": {"workload": "gemma4-e2b-batched-decode (configs[4])", "sequences": batch,
@@ -607,6 +665,9 @@ def main():
                     help="skip the size-matched streaming floor per op")
     ap.add_argument("--floor-sweep", action="store_true",
                     help="time the streaming floor alone over the ops' sizes (one JSON line per size)")
+    ap.add_argument("--policy-sweep", action="store_true",
+                    help="the streaming kernel over every load x store cache policy and two grid shapes at the ops' "
+                         "sizes (one JSON line per size)")
     ap.add_argument("--only", default="", help="comma-separated op subset: per-op timing only (profiling)")
     ap.add_argument("--copy-mib", type=int, default=0, help="also time a device-to-device copy of this size")
     ap.add_argument("--config", choices=["c3c4", "c1", "c2", "gemv", "kv", "logits"], default="c3c4",
@@ -615,6 +676,8 @@ def main():
                          "logits: the soft cap + argmax decode tail -- instead of the headline")
     ap.add_argument("--decode", action="store_true",
                     help="BASELINE configs[4] batched decode (per-layer latency, eager and HIP graph) instead")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="--decode: eager launches only (for tracing tools that do not follow graph replays)")
     ap.add_argument("--batch", type=int, default=256,
                     help="--decode: sequences per step (256 = configs[4]; 1 = the single-sequence decode the "
                          "reference publishes per-token figures for)")
@@ -635,9 +698,13 @@ def main():
         floor_sweep(rt, args.op_iters)
         rt.close()
         return
+    if args.policy_sweep:
+        policy_sweep(rt, args.op_iters)
+        rt.close()
+        return
     floor = None if args.no_floor else StreamFloor(rt)
     if args.decode:
-        print(json.dumps(decode_bench(rt, min(args.steps, 50), min(args.warmup, 5), args.batch)))
+        print(json.dumps(decode_bench(rt, min(args.steps, 50), min(args.warmup, 5), args.batch, not args.no_graph)))
         rt.close()
         return
     if args.config != "c3c4":
