@@ -56,6 +56,33 @@ __global__ __launch_bounds__(kThreads) void stream_floor_kernel(const void* __re
     }
 }
 
+// The token gather's dependency chain with no decode: one wavefront per
+// token (four per workgroup) reads the token's id (scalar load), then the
+// table row it names (16 bytes per lane, lanes past the row re-read it
+// modulo its length), then writes out_row4 float4 of the output row, each a
+// copy of the lane's loaded chunk -- the id round trip, the row round trip
+// and the output stream a quantized gather cannot avoid.
+__global__ __launch_bounds__(256) void gather_floor_kernel(const void* __restrict__ table, uint32_t table_bytes,
+                                                           uint32_t row_bytes, const uint32_t* __restrict__ ids,
+                                                           uint32_t tokens, uint32_t vocab, void* __restrict__ out,
+                                                           uint32_t out_row4) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t t = blockIdx.x * 4u + static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+    if (t >= tokens) return;
+    const uint32_t id = ids[t];
+    if (id >= vocab) return;
+    const uint32_t chunks = (row_bytes + 15u) / 16u;
+    const auto rt = rsrc(table, table_bytes);
+    const uint32_t base = id * row_bytes;
+    u32x4 v[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+        v[k] = __builtin_amdgcn_raw_buffer_load_b128(rt, base + 16u * ((lane + 64u * k) % chunks), 0, kPolicyPlain);
+    const auto ro = rsrc(static_cast<uint8_t*>(out) + static_cast<size_t>(t) * out_row4 * 16u, out_row4 * 16u);
+    for (uint32_t c = lane; c < out_row4; c += 64u)
+        __builtin_amdgcn_raw_buffer_store_b128(v[(c >> 6) & 1u], ro, 16u * c, 0, kPolicyNt);
+}
+
 // Launch cost alone: one-wavefront workgroups that touch no memory (the
 // guard never holds: blockDim.x is 64).
 __global__ __launch_bounds__(64) void launch_floor_kernel(float* __restrict__ sink) {
@@ -98,6 +125,21 @@ int atlas_floor_stream_kind(void* stream, const void* in, size_t in_bytes, void*
     else
         hipLaunchKernelGGL((stream_floor_kernel<kPolicyPlain, kPolicyNt>), dim3(full), dim3(kThreads), 0, s, in, in4,
                            out, out4, sink);
+    return static_cast<int>(hipGetLastError());
+}
+
+// Enqueue one gather floor launch: `tokens` ids into a table of `vocab` rows
+// of `row_bytes` (<= 2048), writing out_row_bytes (a multiple of 16) per
+// token.  The table must hold vocab * row_bytes < 4 GiB.
+int atlas_floor_gather(void* stream, const void* table, uint32_t row_bytes, uint32_t vocab, const uint32_t* ids,
+                       uint32_t tokens, void* out, uint32_t out_row_bytes) {
+    const uint64_t table_bytes = static_cast<uint64_t>(vocab) * row_bytes;
+    if (row_bytes == 0 || row_bytes > 2048 || out_row_bytes % 16 != 0 || table_bytes >= (1ull << 32))
+        return static_cast<int>(hipErrorInvalidValue);
+    if (tokens == 0) return 0;
+    hipLaunchKernelGGL(gather_floor_kernel, dim3((tokens + 3) / 4), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       table, static_cast<uint32_t>(table_bytes), row_bytes, ids, tokens, vocab, out,
+                       out_row_bytes / 16);
     return static_cast<int>(hipGetLastError());
 }
 

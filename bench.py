@@ -56,6 +56,30 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+class Arena:
+    """One device allocation made before anything is timed and kept until the
+    bench ends: every op's rotating buffer sets and the streaming floor's
+    buffers are carved from it.  On MI355X a buffer allocated after others
+    were freed measured up to 3.5 % slower for the same kernel (qk_norm_rope
+    at T=4096: 14.92 us against 14.39 us on a fresh allocation), so per-op
+    allocate/free would make each op's time depend on the ops timed before
+    it."""
+
+    def __init__(self, rt, nbytes):
+        self.rt = rt
+        self.nbytes = nbytes
+        self.buf = rt.alloc(nbytes)
+
+    def region(self, nbytes):
+        if nbytes > self.nbytes:
+            raise RuntimeError(f"bench arena holds {self.nbytes} bytes, {nbytes} requested")
+        return self.buf
+
+
+def _align(n, a=4096):
+    return -(-max(n, 16) // a) * a
+
+
 class Ops:
     """The step's ops: host inputs, algorithmic bytes and launchers."""
 
@@ -114,32 +138,38 @@ class Ops:
             return written[name]
         return sum(n * 4 for n in self.table[name][1].values())
 
-    def build_sets(self, rt, names, nsets):
-        """`nsets` buffer sets holding every input/output of `names`.  Set 0 is
-        uploaded; the others are device-to-device copies at distinct addresses."""
+    def _layout(self, names):
         keys = sorted({k for n in names for k in self.table[n][0]})
         outs = {}
         for n in names:
             outs.update(self.table[n][1])
-        master = {k: rt.upload(self.host[k]) for k in keys}
-        sets = [master]
-        for _ in range(1, nsets):
-            s = {}
+        layout, off = {}, 0
+        for k, nb, dt in ([(k, self.host[k].nbytes, self.host[k].dtype) for k in keys]
+                          + [(k, n * 4, np.dtype(np.float32)) for k, n in outs.items()]):
+            layout[k] = (off, dt)
+            off += _align(nb)
+        return keys, layout, off
+
+    def sets_bytes(self, names, nsets):
+        return nsets * self._layout(names)[2]
+
+    def build_sets(self, rt, names, nsets, arena):
+        """`nsets` buffer sets holding every input/output of `names`, carved
+        from `arena` (one set after another, tensors at 4 KiB-aligned offsets).
+        Set 0 is uploaded; the others are device-to-device copies."""
+        keys, layout, per_set = self._layout(names)
+        base = arena.region(nsets * per_set)
+        sets = []
+        for i in range(nsets):
+            s = {k: base.offset(i * per_set + o, dt) for k, (o, dt) in layout.items()}
             for k in keys:
-                b = rt.alloc(master[k].nbytes, master[k].dtype)
-                rt.copy(b, master[k], master[k].nbytes)
-                s[k] = b
+                if i == 0:
+                    s[k].upload(self.host[k])
+                else:
+                    rt.copy(s[k], sets[0][k], self.host[k].nbytes)
             sets.append(s)
-        for s in sets:
-            for k, n in outs.items():
-                s[k] = rt.empty(n)
         rt.sync()
         return sets
-
-    def free_sets(self, rt, sets):
-        for s in sets:
-            for b in s.values():
-                rt.free(b)
 
 
 class ConfigOps(Ops):
@@ -290,7 +320,7 @@ class StreamFloor:
     path and the memory system give for that many bytes at that size, with no
     arithmetic, reduction or gather."""
 
-    def __init__(self, rt):
+    def __init__(self, rt, arena):
         import ctypes
 
         path = os.path.join(ROOT, "atlas_amd", "libatlas_stream_floor.so")
@@ -303,9 +333,18 @@ class StreamFloor:
         self.lib.atlas_floor_kinds.restype = ctypes.c_int
         self.lib.atlas_floor_launch.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p]
         self.lib.atlas_floor_launch.restype = ctypes.c_int
+        self.lib.atlas_floor_gather.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32,
+                                                ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint32]
+        self.lib.atlas_floor_gather.restype = ctypes.c_int
         self.rt = rt
+        self.arena = arena
         self.stream = rt.lib.atlas_hip_get_stream(rt.ctx)
         self.sink = rt.alloc(256)
+
+    @staticmethod
+    def pool_bytes(in_bytes, out_bytes):
+        per_set = (in_bytes + 255) // 256 * 256 + (out_bytes + 255) // 256 * 256
+        return max(4, math.ceil(ROTATION_BYTES / per_set)) * per_set
 
     def us(self, in_bytes, out_bytes, iters):
         return min(self.us_kinds(in_bytes, out_bytes, iters).values())
@@ -316,7 +355,7 @@ class StreamFloor:
         ib, ob = (in_bytes + 255) // 256 * 256, (out_bytes + 255) // 256 * 256
         per_set = ib + ob
         nsets = max(4, math.ceil(ROTATION_BYTES / per_set))
-        pool = rt.alloc(nsets * per_set)
+        pool = self.arena.region(nsets * per_set)
         rt.memset(pool, 0, nsets * per_set)
         result = {}
         for kind in range(self.lib.atlas_floor_kinds()):
@@ -337,8 +376,31 @@ class StreamFloor:
             rt.record(b)
             rt.sync()
             result[kind] = rt.elapsed_ms(a, b) / iters * 1e3
-        rt.free(pool)
         return result
+
+    def gather_us(self, sets, table, ids, out, row_bytes, vocab, tokens, out_row_bytes, iters):
+        """The token gather's dependency chain without its decode (id, then
+        row, then the output row) on an op's own rotating sets: what a
+        gather of these rows can reach at this size."""
+        rt = self.rt
+
+        def launch(i):
+            s = sets[i % len(sets)]
+            rc = self.lib.atlas_floor_gather(self.stream, s[table].ptr, row_bytes, vocab, s[ids].ptr, tokens,
+                                             s[out].ptr, out_row_bytes)
+            if rc != 0:
+                raise RuntimeError(f"gather floor launch failed: HIP error {rc}")
+
+        for i in range(3):
+            launch(i)
+        rt.sync()
+        a, b = rt.event(), rt.event()
+        rt.record(a)
+        for i in range(iters):
+            launch(i)
+        rt.record(b)
+        rt.sync()
+        return rt.elapsed_ms(a, b) / iters * 1e3
 
     def launch_us(self, blocks, iters):
         """Back-to-back launches of `blocks` empty one-wavefront workgroups."""
@@ -362,6 +424,8 @@ class StreamFloor:
 
 
 POLICY_NAMES = ["plain", "nt", "sc1", "sc1+nt", "sc0+sc1+nt"]
+# token gathers timed against the gather floor too: (table, output, Q6_K)
+GATHER_FLOOR = {"embed_q4_0": ("q4", "e4", False), "embed_q6_k": ("q6", "e6", True)}
 
 
 def policy_sweep(rt, iters):
@@ -370,19 +434,20 @@ def policy_sweep(rt, iters):
     floor's three shapes."""
     import ctypes
 
-    floor = StreamFloor(rt)
+    sizes = [("rms", 25.2, 25.2), ("gather", 3.5, 25.2), ("residual", 50.3, 25.2), ("qk", 42.0, 37.7),
+             ("geglu", 201.3, 100.7)]
+    arena = Arena(rt, max(StreamFloor.pool_bytes(int(r * 1e6), int(w * 1e6)) for _, r, w in sizes))
+    floor = StreamFloor(rt, arena)
     lib = floor.lib
     lib.atlas_floor_stream_policy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
                                               ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                               ctypes.c_uint32]
     lib.atlas_floor_stream_policy.restype = ctypes.c_int
-    sizes = [("rms", 25.2, 25.2), ("gather", 3.5, 25.2), ("residual", 50.3, 25.2), ("qk", 42.0, 37.7),
-             ("geglu", 201.3, 100.7)]
     for name, r_mb, w_mb in sizes:
         ib, ob = int(r_mb * 1e6) // 256 * 256, int(w_mb * 1e6) // 256 * 256
         per_set = ib + ob
         nsets = max(4, math.ceil(ROTATION_BYTES / per_set))
-        pool = rt.alloc(nsets * per_set)
+        pool = arena.region(nsets * per_set)
         rt.memset(pool, 0, nsets * per_set)
         res = {}
         for grid in (0, 4096):
@@ -405,7 +470,6 @@ def policy_sweep(rt, iters):
                     rt.sync()
                     res[f"{'full' if grid == 0 else grid}/{POLICY_NAMES[lp]}/{POLICY_NAMES[sp]}"] = round(
                         rt.elapsed_ms(a, b) / iters * 1e3, 3)
-        rt.free(pool)
         best = min(res, key=res.get)
         print(json.dumps({"size": name, "read_MB": r_mb, "write_MB": w_mb, "best": best, "best_us": res[best],
                           "best_frac": round((ib + ob) / (res[best] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
@@ -423,11 +487,11 @@ def floor_fields(floor, nbytes, out_bytes, op_us, iters):
 def floor_sweep(rt, iters):
     """The floor alone over the sizes the ops move (read MB, write MB): one JSON
     line per size, for the committed floor summary."""
-    floor = StreamFloor(rt)
-    for blocks in (256, 4096, 16384):
-        print(json.dumps({"empty_workgroups": blocks, "us": round(floor.launch_us(blocks, iters), 3)}), flush=True)
     sizes = [(1.57, 1.57), (6.3, 6.3), (12.6, 12.6), (25.2, 0.0), (0.0, 25.2), (3.5, 25.2), (25.2, 25.2),
              (16.8, 16.8), (42.0, 37.7), (50.3, 25.2), (67.1, 33.6), (201.3, 100.7), (171.1, 143.2)]
+    floor = StreamFloor(rt, Arena(rt, max(StreamFloor.pool_bytes(int(r * 1e6), int(w * 1e6)) for r, w in sizes)))
+    for blocks in (256, 4096, 16384):
+        print(json.dumps({"empty_workgroups": blocks, "us": round(floor.launch_us(blocks, iters), 3)}), flush=True)
     for r_mb, w_mb in sizes:
         ib, ob = int(r_mb * 1e6) // 16 * 16, int(w_mb * 1e6) // 16 * 16
         kinds = floor.us_kinds(ib, ob, iters)
@@ -702,25 +766,40 @@ def main():
         policy_sweep(rt, args.op_iters)
         rt.close()
         return
-    floor = None if args.no_floor else StreamFloor(rt)
     if args.decode:
         print(json.dumps(decode_bench(rt, min(args.steps, 50), min(args.warmup, 5), args.batch, not args.no_graph)))
         rt.close()
         return
+
+    def arena_for(o, nsets_of, names, step_sets=0):
+        """The arena every timed region below carves its buffers from."""
+        need = [o.sets_bytes([n], nsets_of(n)) for n in names]
+        if step_sets:
+            need.append(o.sets_bytes(list(o.table), step_sets))
+        if not args.no_floor:
+            need += [StreamFloor.pool_bytes(o.table[n][2] - min(o.out_bytes(n), o.table[n][2]),
+                                            min(o.out_bytes(n), o.table[n][2])) for n in names]
+        arena = Arena(rt, max(need))
+        return arena, None if args.no_floor else StreamFloor(rt, arena)
+
     if args.config != "c3c4":
         from atlas_amd import rope_tables_llama
 
         cops = ConfigOps(wl, rope_tables_llama, args.config)
+        # the weight-streaming projections need >= 1 GiB of distinct weights
+        # to keep the 256 MB MALL out of the measurement
+        cap = 1024 if args.config in ("gemv", "kv", "logits") else 64
+
+        def cnsets(name):
+            return min(cap, max(4, math.ceil(ROTATION_BYTES / cops.set_bytes(name))))
+
+        arena, floor = arena_for(cops, cnsets, list(cops.table))
         per_op = {}
         for name, (_, _, nbytes, launch) in cops.table.items():
-            # the weight-streaming projections need >= 1 GiB of distinct weights
-            # to keep the 256 MB MALL out of the measurement
-            cap = 1024 if args.config in ("gemv", "kv", "logits") else 64
-            nsets = min(cap, max(4, math.ceil(ROTATION_BYTES / cops.set_bytes(name))))
+            nsets = cnsets(name)
             log(f"timing {args.config} {name} ({nsets} rotating sets)")
-            sets = cops.build_sets(rt, [name], nsets)
+            sets = cops.build_sets(rt, [name], nsets, arena)
             ms = time_launches(rt, launch, sets, args.op_iters)
-            cops.free_sets(rt, sets)
             gbs = nbytes / (ms * 1e-3) / 1e9
             per_op[name] = {"us": round(ms * 1e3, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
                             "frac": round(gbs / HBM_PEAK_GBS, 4),
@@ -737,19 +816,28 @@ def main():
         if o not in ops.table:
             sys.exit(f"unknown op {o}; choose from {', '.join(ops.table)}")
 
+    def nsets_of(name):
+        return max(4, math.ceil(ROTATION_BYTES / ops.set_bytes(name)))
+
+    timed = [n for n in ops.table if not ((only or args.copy_mib) and n not in only)]
+    arena, floor = arena_for(ops, nsets_of, timed, 0 if (only or args.copy_mib) else args.step_sets)
     per_op = {}
-    for name, (_, _, nbytes, launch) in ops.table.items():
-        if (only or args.copy_mib) and name not in only:
-            continue
-        nsets = max(4, math.ceil(ROTATION_BYTES / ops.set_bytes(name)))
+    for name in timed:
+        _, _, nbytes, launch = ops.table[name]
+        nsets = nsets_of(name)
         log(f"timing {name} ({nsets} rotating sets)")
-        sets = ops.build_sets(rt, [name], nsets)
+        sets = ops.build_sets(rt, [name], nsets, arena)
         ms = time_launches(rt, launch, sets, args.op_iters)
-        ops.free_sets(rt, sets)
         gbs = nbytes / (ms * 1e-3) / 1e9
         per_op[name] = {"us": round(ms * 1e3, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
                         "frac": round(gbs / HBM_PEAK_GBS, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
                         "rotating_sets": nsets}
+        if floor is not None and name in GATHER_FLOOR:
+            # on the op's own sets, before the streaming floor reuses the arena
+            tk, ok, q6 = GATHER_FLOOR[name]
+            H = ops.L.hidden
+            gu = floor.gather_us(sets, tk, "ids", ok, wl.q_row_bytes(H, q6), ops.Q.vocab, T, H * 4, args.op_iters)
+            per_op[name].update({"gather_floor_us": round(gu, 3), "of_gather_floor": round(gu / (ms * 1e3), 4)})
         if not (only or args.copy_mib or args.no_floor):
             # the same bytes moved by a plain stream: what launch + memory give at this size
             per_op[name].update(floor_fields(floor, nbytes, ops.out_bytes(name), ms * 1e3, args.op_iters))
@@ -768,7 +856,7 @@ def main():
 
     log("timed steps")
     names = list(ops.table)
-    sets = ops.build_sets(rt, names, args.step_sets)
+    sets = ops.build_sets(rt, names, args.step_sets, arena)
 
     def step(i):
         s = sets[i % len(sets)]

@@ -43,6 +43,7 @@ def test_stream_floor_library_exports():
     path = os.path.join(ROOT, "atlas_amd", "libatlas_stream_floor.so")
     assert os.path.exists(path), "run __graft_entry__.build() first"
     lib = ctypes.CDLL(path)
-    for name in ("atlas_floor_stream_kind", "atlas_floor_kinds", "atlas_floor_launch"):
+    for name in ("atlas_floor_stream_kind", "atlas_floor_kinds", "atlas_floor_launch", "atlas_floor_gather",
+                 "atlas_floor_stream_policy", "atlas_floor_policy_count"):
         assert hasattr(lib, name), name
     assert lib.atlas_floor_kinds() == 3
