@@ -379,7 +379,7 @@ struct FoldScansLds {
     uint32_t e0;
 };
 
-template <int R, int J, int MODE, bool PAR, bool STAGE, bool RUN, int POL = -1>
+template <int R, int J, int MODE, bool PAR, bool STAGE, bool RUN>
 __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
     // Squares of R rows, (hidden/4 + 1) float4 per row.  The load phase is
     // straight-line code (rows past the end and columns past the row width
@@ -561,14 +561,14 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
             const f32x4 v = x[r][j], ww = w[j];
             const f32x4 n{v.x * ir * ww.x, v.y * ir * ww.y, v.z * ir * ww.z, v.w * ir * ww.w};
             if (MODE == kNormPlain || MODE == kNormAddNorm) {
-                st_row<POL>(a.out + base, h * 4u, c, n);
+                st_row<-1>(a.out + base, h * 4u, c, n);
             } else if (MODE == kNormResidual) {
-                if (a.normalized) st_row<POL>(a.normalized + base, h * 4u, c, n);
+                if (a.normalized) st_row<-1>(a.normalized + base, h * 4u, c, n);
                 const f32x4 b = e[r][j];
-                st_row<POL>(a.out + base, h * 4u, c, f32x4{b.x + n.x, b.y + n.y, b.z + n.z, b.w + n.w});
+                st_row<-1>(a.out + base, h * 4u, c, f32x4{b.x + n.x, b.y + n.y, b.z + n.z, b.w + n.w});
             } else {
                 const f32x4 b = e[r][j];
-                st_row<POL>(a.out + base, h * 4u, c,
+                st_row<-1>(a.out + base, h * 4u, c,
                             f32x4{(b.x + n.x) * scale, (b.y + n.y) * scale, (b.z + n.z) * scale, (b.w + n.w) * scale});
             }
         }

@@ -779,7 +779,7 @@ def main():
         if not args.no_floor:
             need += [StreamFloor.pool_bytes(o.table[n][2] - min(o.out_bytes(n), o.table[n][2]),
                                             min(o.out_bytes(n), o.table[n][2])) for n in names]
-        arena = Arena(rt, max(need))
+        arena = Arena(rt, max(need, default=1 << 20))
         return arena, None if args.no_floor else StreamFloor(rt, arena)
 
     if args.config != "c3c4":
