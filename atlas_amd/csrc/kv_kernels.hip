@@ -109,13 +109,12 @@ __global__ __launch_bounds__(256) void kv_append_kernel(KvAppendArgs a) {
     extern __shared__ __align__(16) float sq[];  // kv_width squares of V (VNORM)
     __shared__ float inv_shared;
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
-    const uint32_t position = a.positions[t];
-    if (position >= a.capacity) return;  // workgroup-uniform
     const uint32_t w = a.kv_width;
     const float* key = a.key + static_cast<size_t>(t) * w;
     const float* value = a.value + static_cast<size_t>(t) * w;
     const uint32_t passes = (w + kThreads - 1) / kThreads;
 
+    // the row's loads go out before the position's round trip returns
     float k[P], v[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -124,6 +123,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(KvAppendArgs a) {
         k[p] = in ? key[i] : 0.0f;
         v[p] = in ? value[i] : 0.0f;
     }
+    __asm__ volatile("" ::: "memory");  // keeps the loads above the position test
+    const uint32_t position = a.positions[t];
+    if (position >= a.capacity) return;  // workgroup-uniform
     if (VNORM) {
 #pragma unroll
         for (int p = 0; p < P; ++p) {
@@ -298,12 +300,15 @@ __global__ __launch_bounds__(256) void kv_append_row_kernel(KvAppendArgs a) {
     const bool is_v = (wave & 1u) != 0;
     const uint32_t t = blockIdx.x * 2 + (wave >> 1);
     if (t >= a.tokens) return;
-    const uint32_t position = a.positions[t];
-    if (position >= a.capacity) return;
+    // the row's loads go out before the position's round trip returns (a
+    // skipped position only discards them)
     const f32x4* src = reinterpret_cast<const f32x4*>((is_v ? a.value : a.key) + static_cast<size_t>(t) * kW);
     f32x4 x[V4];
 #pragma unroll
     for (int i = 0; i < V4; ++i) x[i] = __builtin_nontemporal_load(src + lane + 64u * i);
+    __asm__ volatile("" ::: "memory");  // keeps the loads above the position test
+    const uint32_t position = a.positions[t];
+    if (position >= a.capacity) return;
     uint8_t* dst = a.cache + (static_cast<size_t>(is_v ? a.capacity : 0u) + position) * kRowBytes;
     if (VNORM && is_v) {
         f32x4* sqw = sq[wave >> 1];
