@@ -554,23 +554,37 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
         const float ir = PAR ? inverse_rms(__uint_as_float(sb[r]), static_cast<float>(h), a.epsilon)
                              : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
         const size_t base = static_cast<size_t>(row0 + r) * h;
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
+        f32x4 n[J];
+        auto emit = [&](int j) {
             const uint32_t c = lane + 64u * j;
-            if (c >= nv) continue;
             const f32x4 v = x[r][j], ww = w[j];
-            const f32x4 n{v.x * ir * ww.x, v.y * ir * ww.y, v.z * ir * ww.z, v.w * ir * ww.w};
+            n[j] = f32x4{v.x * ir * ww.x, v.y * ir * ww.y, v.z * ir * ww.z, v.w * ir * ww.w};
             if (MODE == kNormPlain || MODE == kNormAddNorm) {
-                st_row<-1>(a.out + base, h * 4u, c, n);
+                stg_nt(a.out + base + 4 * c, n[j]);
             } else if (MODE == kNormResidual) {
-                if (a.normalized) st_row<-1>(a.normalized + base, h * 4u, c, n);
-                const f32x4 b = e[r][j];
-                st_row<-1>(a.out + base, h * 4u, c, f32x4{b.x + n.x, b.y + n.y, b.z + n.z, b.w + n.w});
+                const f32x4 b = e[r][j], q = n[j];
+                stg_nt(a.out + base + 4 * c, f32x4{b.x + q.x, b.y + q.y, b.z + q.z, b.w + q.w});
             } else {
-                const f32x4 b = e[r][j];
-                st_row<-1>(a.out + base, h * 4u, c,
-                            f32x4{(b.x + n.x) * scale, (b.y + n.y) * scale, (b.z + n.z) * scale, (b.w + n.w) * scale});
+                const f32x4 b = e[r][j], q = n[j];
+                stg_nt(a.out + base + 4 * c,
+                       f32x4{(b.x + q.x) * scale, (b.y + q.y) * scale, (b.z + q.z) * scale, (b.w + q.w) * scale});
             }
+        };
+        // a row that fills every lane's J float4 stores straight-line code;
+        // one that does not guards each float4
+        const bool full = nv == 64u * J;
+        if (full) {
+#pragma unroll
+            for (int j = 0; j < J; ++j) emit(j);
+        } else {
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if (lane + 64u * j < nv) emit(j);
+        }
+        if (MODE == kNormResidual && a.normalized) {
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if (full || lane + 64u * j < nv) stg_nt(a.normalized + base + 4 * (lane + 64u * j), n[j]);
         }
     }
 }

@@ -170,6 +170,14 @@ class GemmaDecodeStep:
             self.graph = None
 
     # -- accounting --------------------------------------------------------
+    def written_bytes(self) -> dict:
+        """Bytes each op writes (its outputs once), by op name."""
+        S = self.S
+        B, H, QH, D, F, L, W = S.batch, S.hidden, S.q_heads, S.head_dim, S.ffn, S.layers, S.ple_width
+        return {"embed_q4_0": B * H * 4, "ple_q4_0": B * L * W * 4, "qk_norm_rope": B * (QH + 1) * D * 4,
+                "rms_residual_attn": B * H * 4, "geglu": B * F * 4, "rms_residual_ffn": B * H * 4,
+                "geglu_offset_ple": B * W * 4, "rms_add_scale_ple": B * H * 4}
+
     def bytes_per_layer(self) -> int:
         """Algorithmic HBM bytes of one layer's six ops (inputs once, outputs once)."""
         return sum(b for _, b, _ in self.layer_ops(0))

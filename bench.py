@@ -402,6 +402,55 @@ class StreamFloor:
         rt.sync()
         return rt.elapsed_ms(a, b) / iters * 1e3
 
+    def calls_us(self, in_bytes, out_bytes, n, distinct, iters, graphs=True):
+        """Microseconds per launch of every shape, {kind: us}, when n launches
+        run back to back as one HIP graph (or eagerly), over n distinct buffer
+        pairs (distinct) or one: the way the decode step's ops are timed."""
+        rt = self.rt
+        ib, ob = (in_bytes + 255) // 256 * 256, (out_bytes + 255) // 256 * 256
+        per_set = ib + ob
+        sets = n if distinct else 1
+        pool = self.arena.region(sets * per_set)
+        rt.memset(pool, 0, sets * per_set)
+        result = {}
+        for kind in range(self.lib.atlas_floor_kinds()):
+            def launch(i):
+                base = pool.ptr + (i % sets) * per_set
+                rc = self.lib.atlas_floor_stream_kind(self.stream, base, in_bytes, base + ib, out_bytes,
+                                                      self.sink.ptr, kind)
+                if rc != 0:
+                    raise RuntimeError(f"stream floor launch failed: HIP error {rc}")
+
+            g = None
+            if graphs:
+                rt.graph_begin()
+                try:
+                    for i in range(n):
+                        launch(i)
+                finally:
+                    g = rt.graph_end()
+
+            def run():
+                if g is not None:
+                    rt.graph_launch(g)
+                else:
+                    for i in range(n):
+                        launch(i)
+
+            for _ in range(3):
+                run()
+            rt.sync()
+            a, b = rt.event(), rt.event()
+            rt.record(a)
+            for _ in range(iters):
+                run()
+            rt.record(b)
+            rt.sync()
+            if g is not None:
+                rt.graph_destroy(g)
+            result[kind] = rt.elapsed_ms(a, b) / (iters * n) * 1e3
+        return result
+
     def launch_us(self, blocks, iters):
         """Back-to-back launches of `blocks` empty one-wavefront workgroups."""
         rt = self.rt
@@ -609,7 +658,7 @@ M2_MAX_CONTEXT = {
 }
 
 
-def decode_bench(rt, steps, warmup, batch=256, graphs=True):
+def decode_bench(rt, steps, warmup, batch=256, graphs=True, floor=True):
     """`batch` sequences x 1 token (256 by default; 1 for
     the single-sequence decode the reference publishes), 35 layers of the
     fused ops in the reference decode order (atlas_amd.decode), eager and as
@@ -669,6 +718,19 @@ def decode_bench(rt, steps, warmup, batch=256, graphs=True):
         per_op[name] = {"us": round(us, 3), "bytes": nbytes, "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
                         "per": "layer"}
     head_us = sum(v["us"] for v in per_op.values() if v["per"] == "step")
+    if floor:
+        # each op against the streaming floor of its own bytes, timed the same
+        # way: L launches as one graph, over L distinct buffers for the
+        # per-layer ops and one buffer for the per-step gathers (as above)
+        written = step.written_bytes()
+        need = max((L if v["per"] == "layer" else 1) * ((v["bytes"] - written[k] + 255) // 256 * 256
+                                                       + (written[k] + 255) // 256 * 256)
+                   for k, v in per_op.items())
+        fl = StreamFloor(rt, Arena(rt, need))
+        for k, v in per_op.items():
+            out_b = min(written[k], v["bytes"])
+            fu = min(fl.calls_us(v["bytes"] - out_b, out_b, L, v["per"] == "layer", steps, graphs).values())
+            v.update({"floor_us": round(fu, 3), "of_floor": round(fu / v["us"], 4)})
     step.close()
     per_layer = (graph_us - head_us) / L
     mode = "graph replay" if graphs else "eager launches"
@@ -767,7 +829,8 @@ def main():
         rt.close()
         return
     if args.decode:
-        print(json.dumps(decode_bench(rt, min(args.steps, 50), min(args.warmup, 5), args.batch, not args.no_graph)))
+        print(json.dumps(decode_bench(rt, min(args.steps, 50), min(args.warmup, 5), args.batch, not args.no_graph,
+                                      not args.no_floor)))
         rt.close()
         return
 
