@@ -380,15 +380,16 @@ struct FoldScansLds {
 };
 
 template <int R, int J, int MODE, bool PAR, bool STAGE, bool RUN>
-__global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
+__global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
     // Squares of R rows, (hidden/4 + 1) float4 per row.  The load phase is
     // straight-line code (rows past the end and columns past the row width
     // are clamped to valid duplicate addresses and never stored), so the
     // compiler can wait for chunk j's loads alone before folding it.
     extern __shared__ f32x4 sq4[];
     constexpr bool kOperand = MODE != kNormPlain;
-    // RUN: one row; a second wavefront computes the continuation's scans
-    // (fold_scan_ahead) while the first folds the in-order head
+    // RUN: one row; two more wavefronts compute the continuation's scans
+    // (fold_scan_ahead, two binades each) while the first folds the
+    // in-order head
     constexpr bool kRun = RUN && PAR && J > 1 && R == 1;
     constexpr int kRunS = 4 * (J > 1 ? J - 1 : 1);
     const uint32_t lane = threadIdx.x & 63u;
@@ -414,7 +415,8 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
         }
     };
     if constexpr (kRun) {
-        if (threadIdx.x >= 64) {  // the helper wavefront
+        if (threadIdx.x >= 64) {  // the two helper wavefronts, two binades each
+            const uint32_t b0 = 2u * (static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) - 1u);
             __syncthreads();  // every square staged
             const f32x4 h0 = sq4[lane];
             const float approx = wave_sum_any_order_f32((h0.x + h0.y) + (h0.z + h0.w));
@@ -423,16 +425,16 @@ __global__ __launch_bounds__(RUN ? 128 : 64) void rms_reg_kernel(NormArgs a) {
             const uint32_t e0 = __float_as_uint(approx * 0.999f) >> 23;
             float run[kRunS];
             read_run(run);
-            const FoldScans<4> f = fold_scan_ahead<kRunS, 4>(run, e0);
+            const FoldScans<2> f = fold_scan_ahead<kRunS, 2>(run, e0 + b0);
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                scans_lds->inc[b][lane] = f.inc[b];
-                scans_lds->incl[b][lane] = f.incl[b];
+            for (int b = 0; b < 2; ++b) {
+                scans_lds->inc[b0 + b][lane] = f.inc[b];
+                scans_lds->incl[b0 + b][lane] = f.incl[b];
             }
             if (lane == 0) {
 #pragma unroll
-                for (int b = 0; b < 4; ++b) scans_lds->bad[b] = f.bad[b];
-                scans_lds->e0 = e0;
+                for (int b = 0; b < 2; ++b) scans_lds->bad[b0 + b] = f.bad[b];
+                if (b0 == 0) scans_lds->e0 = e0;
             }
             __syncthreads();  // scans published
             return;
@@ -610,10 +612,13 @@ RegConfig pick_reg(uint32_t rows, int mode) {
     return RegConfig{1, true};
 }
 
-// The continuation as one run with its scans computed ahead by a helper
-// wavefront (RUN).  Measured on MI355X: decode batches gain (C5 step at 256
-// rows: 29.5 -> 28.5 us per layer); from 2048 rows up the second wavefront
-// per row costs more than it hides ([4096, 1536]: 10.3 -> 13.9 us).
+// The continuation as one run with its scans computed ahead by helper
+// wavefronts (RUN).  Measured on MI355X: decode batches gain (C5 step at 256
+// rows: 29.5 -> 28.5 us per layer with one helper computing four binades,
+// 27.8 -> 26.8 with two helpers of two binades each, whose scans then land
+// before the head's in-order fold ends); from 2048 rows up the extra
+// wavefronts per row cost more than they hide ([4096, 1536]: 10.3 -> 13.9 us
+// with one helper).
 bool norm_run(uint32_t rows) { return rows < 2048; }
 
 template <int R, int J, int MODE>
@@ -629,7 +634,7 @@ hipError_t launch_reg_rj(hipStream_t s, const NormArgs& a, bool par) {
     const dim3 grid((a.rows + R - 1) / R);
     if constexpr (R == 1 && J > 1) {
         if (run) {
-            hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, true>), grid, dim3(2 * kWave), lds, s, a);
+            hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, true>), grid, dim3(3 * kWave), lds, s, a);
             return hipGetLastError();
         }
     }
