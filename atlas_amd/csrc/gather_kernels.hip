@@ -46,12 +46,11 @@ __device__ __forceinline__ void q4_0_decode4(const uint8_t* row, uint32_t col, f
     const uint32_t off = blk + 2 + (k & 15);  // even
     const uint32_t lo = lds_u16(row + off), hi = lds_u16(row + off + 2);
     const uint32_t bytes = lo | (hi << 16);
-    const uint32_t shift = k < 16 ? 0 : 4;
+    // the four nibbles as the bytes of one word; float(nib - 8) ==
+    // float(nib) - 8 exactly
+    const uint32_t nibs = (bytes >> (k < 16 ? 0 : 4)) & 0x0f0f0f0fu;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int nib = static_cast<int>((bytes >> (8 * j + shift)) & 15u);
-        v[j] = static_cast<float>(nib - 8) * d;
-    }
+    for (int j = 0; j < 4; ++j) v[j] = (static_cast<float>((nibs >> (8 * j)) & 0xffu) - 8.0f) * d;
 }
 
 // Four consecutive Q8_0 values starting at column `col` (col % 4 == 0):
@@ -79,12 +78,14 @@ __device__ __forceinline__ void q6_k_decode4(const uint8_t* row, uint32_t col, f
     const float sc = static_cast<float>(static_cast<int8_t>(row[blk + 192 + half * 8 + (l >> 4) + 2 * st]));
     const float d = h2f(static_cast<uint16_t>(lds_u16(row + blk + 208)));
     const uint32_t lshift = st >= 2 ? 4 : 0;
+    // the four 6-bit codes as the bytes of one word: low nibbles and high
+    // bit pairs extracted four at a time (q_j = byte j, 0..63)
+    const uint32_t codes = ((ql >> lshift) & 0x0f0f0f0fu) | (((qh >> (2 * st)) & 0x03030303u) << 4);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const uint32_t low = (ql >> (8 * j + lshift)) & 15u;
-        const uint32_t high = (qh >> (8 * j + 2 * st)) & 3u;
-        const int q = static_cast<int>((high << 4) | low) - 32;
-        v[j] = static_cast<float>(q) * sc * d;
+        // float(q - 32) == float(q) - 32 exactly (small integers)
+        const float q = static_cast<float>((codes >> (8 * j)) & 0xffu) - 32.0f;
+        v[j] = q * sc * d;
     }
 }
 
