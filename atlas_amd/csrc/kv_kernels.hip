@@ -328,6 +328,61 @@ __global__ __launch_bounds__(256) void kv_append_row_kernel(KvAppendArgs a) {
     store_row<FMT, V4>(x, dst, rowbuf[wave], lane, kRowBytes);
 }
 
+// V-norm appends of many tokens at kv_width 256: eight tokens per
+// workgroup, two per wavefront.  Lanes 0..7 of wavefront 0 fold the eight V
+// rows' squares in index order in one instruction stream (each lane's fold
+// is the per-token kernel's, so the bits are the same) while every
+// wavefront encodes and stores its K rows; the V rows are scaled and encoded
+// once their inverse RMS is published.  A token at a position past the
+// capacity (or past the last token) stores nothing.
+template <int FMT>
+__global__ __launch_bounds__(256) void kv_append_rows8_kernel(KvAppendArgs a) {
+    constexpr uint32_t kW = 256;
+    constexpr uint32_t kRowBytes = FMT == kKvF32 ? kW * 4 : (kW / 32) * (FMT == kKvQ8_0 ? 34u : 18u);
+    // V squares, one row per token; a 65-float4 stride puts the eight rows
+    // that lanes 0..7 read together on distinct LDS banks
+    __shared__ __align__(16) f32x4 sq[8][65];
+    __shared__ float inv_lds[8];
+    __shared__ __align__(16) uint8_t rowbuf[4][FMT == kKvF32 ? 16 : kRowBytes];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+    const uint32_t tb = blockIdx.x * 8u + 2u * wave;  // this wavefront's tokens tb, tb + 1
+    f32x4 k[2][1], v[2][1];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const size_t t = min(tb + i, a.tokens - 1);  // loads of a token past the end are clamped, never stored
+        k[i][0] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a.key + t * kW) + lane);
+        v[i][0] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a.value + t * kW) + lane);
+    }
+    __asm__ volatile("" ::: "memory");  // keeps the loads above the position reads
+    uint32_t position[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) position[i] = tb + i < a.tokens ? a.positions[tb + i] : a.capacity;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const f32x4 x = v[i][0];
+        sq[2 * wave + i][lane] = f32x4{x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w};
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 8) inv_lds[lane] = inverse_rms(fold_lds_chunk(sq[lane], 64u, 0.0f), static_cast<float>(kW),
+                                                           a.epsilon);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        if (position[i] < a.capacity)
+            store_row<FMT, 1>(k[i], a.cache + static_cast<size_t>(position[i]) * kRowBytes, rowbuf[wave], lane,
+                              kRowBytes);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        if (position[i] >= a.capacity) continue;
+        const float inv = inv_lds[2 * wave + i];
+        const f32x4 x = v[i][0];
+        const f32x4 y[1] = {f32x4{x.x * inv, x.y * inv, x.z * inv, x.w * inv}};
+        store_row<FMT, 1>(y, a.cache + (static_cast<size_t>(a.capacity) + position[i]) * kRowBytes, rowbuf[wave],
+                          lane, kRowBytes);
+    }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <int FMT>
@@ -335,6 +390,10 @@ bool launch_row(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
     const uint32_t w = a.kv_width;
     if ((w != 256 && w != 512 && w != 1024) || !aligned16(a.key) || !aligned16(a.value) || !aligned16(a.cache))
         return false;
+    if (vnorm && w == 256 && a.tokens >= 256) {
+        hipLaunchKernelGGL((kv_append_rows8_kernel<FMT>), dim3((a.tokens + 7) / 8), dim3(256), 0, stream, a);
+        return true;
+    }
     const dim3 grid((a.tokens + 1) / 2);
 #define ATLAS_KV_ROW(V)                                                                          \
     if (vnorm)                                                                                   \

@@ -79,11 +79,13 @@ def _values(r, tokens, w, kind):
 
 
 @pytest.mark.parametrize("fmt", ["f32", "q8_0", "q4_0"])
-@pytest.mark.parametrize("w,tokens,cap", [(256, 1, 64), (512, 1, 4096), (256, 4096, 4096), (32, 9, 16),
-                                          (4096, 3, 4), (96, 33, 40), (1024, 130, 128)])
+@pytest.mark.parametrize("w,tokens,cap", [(256, 1, 64), (512, 1, 4096), (256, 4096, 4096), (256, 301, 512),
+                                          (32, 9, 16), (4096, 3, 4), (96, 33, 40), (1024, 130, 128)])
 @pytest.mark.parametrize("kind", ["normal", "adversarial", "nan"])
 def test_kv_append_shapes(rt, ora, fmt, w, tokens, cap, kind):
-    """Decode (one token at a random position), prefill batches, ragged widths,
+    """Decode (one token at a random position), prefill batches (eight tokens
+    per workgroup with the V norm at width 256, a ragged last workgroup at
+    301 tokens), ragged widths,
     positions past the capacity (skipped), adversarial blocks, and NaN blocks
     and rows (the encoders' maximum starts at 0, as the reference's does)."""
     r = np.random.default_rng(w * 7 + tokens + cap)
