@@ -47,3 +47,61 @@ def test_stream_floor_library_exports():
                  "atlas_floor_stream_policy", "atlas_floor_policy_count"):
         assert hasattr(lib, name), name
     assert lib.atlas_floor_kinds() == 3
+
+
+def test_buffer_sets_carved_from_one_arena():
+    """Every op's rotating sets are views into one arena allocation: each
+    tensor 4 KiB aligned, tensors and sets disjoint, set 0 uploaded and the
+    others copied from it, and a request larger than the arena refused."""
+    import numpy as np
+
+    class View:
+        def __init__(self, ptr, nbytes, dtype):
+            self.ptr, self.nbytes, self.dtype = ptr, nbytes, np.dtype(dtype)
+            self.uploaded = None
+
+        def offset(self, off, dtype=None):
+            return View(self.ptr + off, self.nbytes - off, dtype if dtype is not None else self.dtype)
+
+        def upload(self, host):
+            self.uploaded = host.nbytes
+            return self
+
+    class FakeRuntime:
+        def __init__(self):
+            self.copies = []
+
+        def alloc(self, nbytes, dtype=np.float32):
+            return View(1 << 20, nbytes, dtype)
+
+        def copy(self, dst, src, nbytes):
+            self.copies.append((dst.ptr, src.ptr, nbytes))
+
+        def sync(self):
+            pass
+
+    ops = object.__new__(bench.Ops)
+    ops.host = {"x": np.zeros(1000, np.float32), "ids": np.zeros(7, np.uint32)}
+    ops.table = {"op": (["x", "ids"], {"y": 5000}, 0, None)}
+    rt = FakeRuntime()
+    per_set = ops.sets_bytes(["op"], 1)
+    arena = bench.Arena(rt, ops.sets_bytes(["op"], 3))
+    sets = ops.build_sets(rt, ["op"], 3, arena)
+    spans = []
+    for i, s in enumerate(sets):
+        for k, v in s.items():
+            assert (v.ptr - arena.buf.ptr) % 4096 == 0
+            size = ops.host[k].nbytes if k in ops.host else 5000 * 4
+            spans.append((v.ptr, v.ptr + size))
+            assert arena.buf.ptr + i * per_set <= v.ptr and v.ptr + size <= arena.buf.ptr + (i + 1) * per_set
+        assert s["ids"].dtype == np.uint32 and s["y"].dtype == np.float32
+    spans.sort()
+    assert all(a[1] <= b[0] for a, b in zip(spans, spans[1:]))
+    assert sets[0]["x"].uploaded == 4000 and sets[0]["ids"].uploaded == 28
+    assert len(rt.copies) == 2 * 2 and all(n in (4000, 28) for _, _, n in rt.copies)
+    try:
+        ops.build_sets(rt, ["op"], 4, arena)
+    except RuntimeError:
+        pass
+    else:
+        raise AssertionError("a request beyond the arena must be refused")
