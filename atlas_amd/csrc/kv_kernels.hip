@@ -114,7 +114,10 @@ __global__ __launch_bounds__(256) void kv_append_kernel(KvAppendArgs a) {
     const float* value = a.value + static_cast<size_t>(t) * w;
     const uint32_t passes = (w + kThreads - 1) / kThreads;
 
-    // the row's loads go out before the position's round trip returns
+    // the position's load goes out first and the row's right behind it
+    // (loads return in issue order, so the position is waited for alone)
+    const uint32_t position = a.positions[t];
+    __asm__ volatile("" ::: "memory");
     float k[P], v[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -124,7 +127,6 @@ __global__ __launch_bounds__(256) void kv_append_kernel(KvAppendArgs a) {
         v[p] = in ? value[i] : 0.0f;
     }
     __asm__ volatile("" ::: "memory");  // keeps the loads above the position test
-    const uint32_t position = a.positions[t];
     if (position >= a.capacity) return;  // workgroup-uniform
     if (VNORM) {
 #pragma unroll
@@ -187,13 +189,10 @@ __global__ __launch_bounds__(256) void kv_append_kernel(KvAppendArgs a) {
 // block is 8 lanes.  The V sum of squares folds in index order on lane 0 from
 // LDS while the K wavefront encodes and stores; each encoded row is
 // assembled in LDS and written with 16-byte stores (a Q8_0 / Q4_0 row of 256
-// values is 272 / 144 bytes, 16-byte aligned for every position).  Same encoders as above:
-//  * block maximum over 8 lanes: the lane's fmaxf of its 4 |v|, then
-//    quad_perm xor 1, xor 2 and row_half_mirror (fmaxf ignores NaN);
-//  * Q4_0 signed maximum: the first value of the block with |v| == max
-//    (lane order, then position in the lane), or the block's value 0;
-//  * Q4_0 nibble pairing: values j and j + 16 sit in lanes g and g + 4 of
-//    the block, exchanged with an xor-4 swizzle.
+// values is 272 / 144 bytes, 16-byte aligned for every position).  The
+// encoder (encode_items) gives the bits of the per-value engine above; it
+// takes each quotient as a product with the scale's reciprocal where that
+// provably yields the same code.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void lds_wave_handoff() {
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -206,64 +205,184 @@ __device__ __forceinline__ float group8_max(float v) {
     return fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
 }
 
-// Encode the lane's 4 values (block b = lane/8 + 8i, index 4(lane%8)) into
-// the row buffer `row` (LDS, 2-byte stores: blocks are 34 / 18 bytes).
+// Quotient band.  A code depends on the quotient fl(v / scale) only through
+// which pair of consecutive half-integers it lies between (Q8_0 rounds half
+// away from zero, Q4_0 truncates fl(q + 8.5) with q + 8.5 < 17, whose
+// rounding error is below 2^-20).  For a normal scale (|scale| in
+// [2^-126, 2^126]) and |v| <= max|v| of the block, |q| <= 128 and
+// v * rcp(scale) (v_rcp_f32 is within 1 ulp) is within 2^-15 of fl(v /
+// scale); a product more than 2^-12 from every half-integer therefore gives
+// the code of the correctly rounded quotient.  A lane with any product in
+// that band, a scale outside the normal range or a NaN value recomputes its
+// codes with fdiv_rn and the reference's own steps.
+constexpr float kHalfBand = 0x1p-12f;
+
+__device__ __forceinline__ bool scale_normal(float scale) {
+    const float a = __builtin_fabsf(scale);
+    return a >= 0x1p-126f && a <= 0x1p126f;  // false for 0, inf, NaN
+}
+
+__device__ __forceinline__ bool off_half(float q) {  // NaN: false
+    return __builtin_fabsf(__builtin_amdgcn_fractf(q) - 0.5f) > kHalfBand;
+}
+
+// The reference's code steps on the correctly rounded quotient.
 template <int FMT>
-__device__ __forceinline__ void encode4(const f32x4 x, uint8_t* row, uint32_t block, uint32_t g) {
-    const float v[4] = {x.x, x.y, x.z, x.w};
-    // seeded with 0, as the reference's fold is (kernels.metal:1220-1221,
-    // 1244-1245): NaN values never raise it, and an all-NaN block gives 0
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) m = fmaxf(m, __builtin_fabsf(v[i]));
-    const float amax = group8_max(m);
-    uint16_t* dst = reinterpret_cast<uint16_t*>(row + block * (FMT == kKvQ8_0 ? 34u : 18u));
+__device__ __forceinline__ uint32_t code_exact(float v, float scale) {
     if (FMT == kKvQ8_0) {
-        const float scale = amax == 0.0f ? 0.0f : fdiv_rn(amax, 127.0f);
-        uint32_t packed = 0;
+        if (scale == 0.0f) return 0u;
+        return static_cast<uint32_t>(static_cast<int>(roundf(fminf(fmaxf(fdiv_rn(v, scale), -127.0f), 127.0f)))) &
+               0xffu;
+    }
+    if (scale == 0.0f) return 0u;
+    const float t = fdiv_rn(v, scale) + 8.5f;
+    return t >= 15.0f ? 15u : (t > 0.0f ? static_cast<uint32_t>(static_cast<int>(t)) : 0u);
+}
+
+// The same code from a product q outside the band (round to nearest even
+// and round half away agree off the half-integers; trunc of the clamped
+// q + 8.5 is the reference's three-way select).
+template <int FMT>
+__device__ __forceinline__ uint32_t code_fast(float q) {
+    if (FMT == kKvQ8_0)
+        return static_cast<uint32_t>(static_cast<int>(__builtin_rintf(__builtin_amdgcn_fmed3f(q, -127.0f, 127.0f)))) &
+               0xffu;
+    return static_cast<uint32_t>(static_cast<int>(__builtin_amdgcn_fmed3f(q + 8.5f, 0.0f, 15.0f)));
+}
+
+// fl(a / 127) for the Q8_0 scale (a = a block maximum, >= 0).  For a in
+// [2^-100, 2^100], Markstein's correction of the product with c = RN(1/127):
+// q0 = a c, r = a - 127 q0 (exact in an fma), q = RN(q0 + r c) -- equal to
+// RN(a / 127) for every float of one binade, checked exhaustively, and so
+// over the whole range, where every step scales exactly by powers of two.
+// a = 0 gives +0 through the same steps; other values take the IEEE
+// division, on a branch that is not taken for ordinary data (the empty asm
+// keeps the compiler from computing both and selecting).
+__device__ __forceinline__ float div127(float a) {
+    constexpr float c = 1.0f / 127.0f;
+    const float q0 = a * c;
+    float q = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, a), c, q0);
+    if (!(a == 0.0f || (a >= 0x1p-100f && a <= 0x1p100f))) {
+        __asm__ volatile("");
+        q = fdiv_rn(a, 127.0f);
+    }
+    return q;
+}
+
+// Maximum of |v| over a 32-value block held by 8 lanes (4 values each),
+// seeded with 0 as the reference's fold is (kernels.metal:1220-1221,
+// 1244-1245): NaN never raises it and an all-NaN block gives 0.  The lane's
+// fmaxf of its 4 |v|, then quad_perm xor 1, xor 2 and row_half_mirror.
+__device__ __forceinline__ float block_max(const f32x4 x) {
+    float m = 0.0f;
+    m = fmaxf(m, __builtin_fabsf(x.x));
+    m = fmaxf(m, __builtin_fabsf(x.y));
+    m = fmaxf(m, __builtin_fabsf(x.z));
+    m = fmaxf(m, __builtin_fabsf(x.w));
+    return group8_max(m);
+}
+
+// Encode N groups of four values held by the lane: item n is x[n] (times
+// inv[n] when NORM: the V norm's scaling, which the encoder applies itself),
+// values 4g..4g+3 (g = lane % 8) of block blk[n] in the LDS row buffer
+// row[n] (2-byte stores: blocks are 34 / 18 bytes).  bmax[n] is
+// block_max(x[n]); the items' chains are independent and overlap.
+//  * With NORM the block maximum of y = fl(x inv) is fl(bmax inv): rounding
+//    is monotonic, so the largest |x| gives the largest |y|.  Where that
+//    product is not finite (a NaN or inf in the row) the maximum is taken
+//    over y itself.
+//  * Q4_0 signed maximum: the first value of the block with |y| == max
+//    (lane order, then position in the lane) is +max or -max, so only its
+//    sign travels: two ballots, the first hit lane of the group, its bit.
+//  * Quotients: q = x * fl(inv rcp(scale)) (x * rcp(scale) without NORM) is
+//    within 2.75 * 2^-16 of fl(y / scale) for a normal scale and a normal
+//    fl(inv rcp(scale)), so outside the 2^-12 band it gives the reference's
+//    code; each value in the band (or any value when those factors are not
+//    normal) is recomputed with fdiv_rn and the reference's steps.
+//  * Q4_0 nibble pairing: values j and j + 16 sit in lanes g and g + 4 of
+//    the block, exchanged with an xor-4 swizzle.
+typedef __attribute__((address_space(3))) volatile uint16_t lds_u16;
+
+template <int FMT, int N, bool NORM>
+__device__ __forceinline__ void encode_items(const f32x4 (&x)[N], const float (&inv)[N], const float (&bmax)[N],
+                                             uint8_t* const (&row)[N], const uint32_t (&blk)[N], uint32_t g) {
+    float scale[N];
+    uint32_t code[N][4];
+    bool need[N][4];
+    bool any = false;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            int code = 0;
-            if (scale != 0.0f) code = static_cast<int>(roundf(fminf(fmaxf(fdiv_rn(v[i], scale), -127.0f), 127.0f)));
-            packed |= (static_cast<uint32_t>(code) & 0xffu) << (8 * i);
+    for (int n = 0; n < N; ++n) {
+        const float v[4] = {x[n].x, x[n].y, x[n].z, x[n].w};
+        float y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = NORM ? v[i] * inv[n] : v[i];
+        float amax = NORM ? bmax[n] * inv[n] : bmax[n];
+        if (NORM && !__builtin_isfinite(amax)) {  // uniform over the block's 8 lanes
+            float m = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) m = fmaxf(m, __builtin_fabsf(y[i]));
+            amax = group8_max(m);
         }
-        if (g == 0) dst[0] = static_cast<uint16_t>(f16_bits(scale));
-        dst[1 + 2 * g] = static_cast<uint16_t>(packed);
-        dst[2 + 2 * g] = static_cast<uint16_t>(packed >> 16);
-    } else {
-        // first value of this lane with |v| == amax (amax > 0), else value 0
-        float cand = v[0];
-        bool has = false;
+        if (FMT == kKvQ8_0) {
+            scale[n] = div127(amax);  // amax == 0 gives 0, as the reference's select does
+        } else {
+            // sign of this lane's first value with |y| == amax (amax > 0)
+            bool has = false, neg = false;
 #pragma unroll
-        for (int i = 3; i >= 0; --i) {
-            const bool hit = amax > 0.0f && __builtin_fabsf(v[i]) == amax;
-            cand = hit ? v[i] : cand;
-            has = has || hit;
-        }
-        const uint64_t hits = __builtin_amdgcn_ballot_w64(has);
-        const uint32_t base = __lane_id() & ~7u;
-        const uint32_t mine = static_cast<uint32_t>(hits >> base) & 0xffu;
-        const uint32_t src = base + (mine ? static_cast<uint32_t>(__builtin_ctz(mine)) : 0u);
-        const float smax = __int_as_float(__shfl(__float_as_int(cand), static_cast<int>(src), kWave));
-        const float scale = amax == 0.0f ? 0.0f : fdiv_rn(smax, -8.0f);
-        uint32_t packed = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            int code = 0;
-            if (scale != 0.0f) {
-                const float t = fdiv_rn(v[i], scale) + 8.5f;
-                code = t >= 15.0f ? 15 : (t > 0.0f ? static_cast<int>(t) : 0);
+            for (int i = 3; i >= 0; --i) {
+                const bool hit = amax > 0.0f && __builtin_fabsf(y[i]) == amax;
+                neg = hit ? __builtin_signbit(y[i]) != 0 : neg;
+                has = has || hit;
             }
-            packed |= static_cast<uint32_t>(code) << (8 * i);
+            const uint64_t hits = __builtin_amdgcn_ballot_w64(has);
+            const uint64_t negs = __builtin_amdgcn_ballot_w64(has && neg);
+            const uint32_t base = __lane_id() & ~7u;
+            const uint32_t mine = static_cast<uint32_t>(hits >> base) & 0xffu;
+            const uint32_t first = base + (mine ? static_cast<uint32_t>(__builtin_ctz(mine)) : 0u);
+            const float smax = ((negs >> first) & 1u) ? -amax : amax;
+            // smax / -8 is exact up to the final rounding, as the product is
+            scale[n] = amax == 0.0f ? 0.0f : smax * -0.125f;
         }
-        // lane g < 4 of the block holds values 4g..4g+3 (low nibbles), lane
-        // g + 4 the values 16 + 4g.. (high nibbles): xor-4 swizzle
-        const uint32_t partner = static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(packed), 0x101f));
-        if (g == 0) dst[0] = static_cast<uint16_t>(f16_bits(scale));
-        if (g < 4) {
-            const uint32_t bytes = packed | (partner << 4);
-            dst[1 + 2 * g] = static_cast<uint16_t>(bytes);
-            dst[2 + 2 * g] = static_cast<uint16_t>(bytes >> 16);
+        const float r = __builtin_amdgcn_rcpf(scale[n]);
+        const float ir = NORM ? inv[n] * r : r;
+        const bool ok = scale_normal(scale[n]) && (!NORM || scale_normal(ir));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float q = v[i] * ir;
+            need[n][i] = !(ok && off_half(q));
+            code[n][i] = code_fast<FMT>(q);
+            any = any || need[n][i];
+        }
+    }
+    if (any) {
+#pragma unroll
+        for (int n = 0; n < N; ++n) {
+            const float v[4] = {x[n].x, x[n].y, x[n].z, x[n].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (need[n][i]) code[n][i] = code_exact<FMT>(NORM ? v[i] * inv[n] : v[i], scale[n]);
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+        const uint32_t packed = code[n][0] | (code[n][1] << 8) | (code[n][2] << 16) | (code[n][3] << 24);
+        // volatile keeps the 2-byte writes apart: merged, every other block's
+        // pair would be an unaligned 4-byte LDS write, which stalls
+        lds_u16* dst = (lds_u16*)(row[n] + blk[n] * (FMT == kKvQ8_0 ? 34u : 18u));  // generic -> LDS
+        if (FMT == kKvQ8_0) {
+            if (g == 0) dst[0] = f16_bits(scale[n]);
+            dst[1 + 2 * g] = static_cast<uint16_t>(packed);
+            dst[2 + 2 * g] = static_cast<uint16_t>(packed >> 16);
+        } else {
+            // lane g < 4 of the block holds values 4g..4g+3 (low nibbles),
+            // lane g + 4 the values 16 + 4g.. (high nibbles)
+            const uint32_t partner = static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(packed), 0x101f));
+            if (g == 0) dst[0] = f16_bits(scale[n]);
+            if (g < 4) {
+                const uint32_t bytes = packed | (partner << 4);
+                dst[1 + 2 * g] = static_cast<uint16_t>(bytes);
+                dst[2 + 2 * g] = static_cast<uint16_t>(bytes >> 16);
+            }
         }
     }
 }
@@ -277,14 +396,79 @@ __device__ __forceinline__ void store_row(const f32x4 (&x)[V4], uint8_t* dst, ui
         for (int i = 0; i < V4; ++i)
             __builtin_nontemporal_store(x[i], reinterpret_cast<f32x4*>(dst) + lane + 64u * i);
     } else {
+        uint8_t* rows[V4];
+        uint32_t blk[V4];
+        float one[V4], bmax[V4];
 #pragma unroll
-        for (int i = 0; i < V4; ++i) encode4<FMT>(x[i], lds_row, lane / 8u + 8u * i, lane & 7u);
+        for (int i = 0; i < V4; ++i) {
+            rows[i] = lds_row;
+            blk[i] = lane / 8u + 8u * i;
+            one[i] = 1.0f;
+            bmax[i] = block_max(x[i]);
+        }
+        encode_items<FMT, V4, false>(x, one, bmax, rows, blk, lane & 7u);
         lds_wave_handoff();
         const uint32_t n16 = row_bytes / 16;  // <= 68 for V4 <= 4
         for (uint32_t u = lane; u < n16; u += kWave)
             __builtin_nontemporal_store(reinterpret_cast<const f32x4*>(lds_row)[u], reinterpret_cast<f32x4*>(dst) + u);
         lds_wave_handoff();  // the buffer is rewritten by the next row
     }
+}
+
+// Rows of kv_width 256 for the eight-token kernel (one f32x4 per lane per
+// row).  Explicit global casts keep the stores global, not flat: LDS waits
+// do not count global stores, and they do count flat ones.
+typedef __attribute__((address_space(1))) f32x4 global_f32x4;
+
+// Store two f32 rows, scaled by inv[i] when NORM; a row whose `ok` is false
+// stores nothing.
+template <bool NORM>
+__device__ __forceinline__ void store_f32_rows2(const f32x4 (&x)[2], const float (&inv)[2], uint8_t* const (&dst)[2],
+                                                const bool (&ok)[2], uint32_t lane) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const f32x4 y = NORM ? f32x4{x[i].x * inv[i], x[i].y * inv[i], x[i].z * inv[i], x[i].w * inv[i]} : x[i];
+        if (ok[i]) __builtin_nontemporal_store(y, (global_f32x4*)dst[i] + lane);
+    }
+}
+
+// Encode two rows (scaled by inv[i] when NORM; bmax: their block_max before
+// scaling) side by side into the LDS row buffers at `lds`.
+template <int FMT, bool NORM>
+__device__ __forceinline__ void encode_rows2(const f32x4 (&x)[2], const float (&inv)[2], const float (&bmax)[2],
+                                             uint8_t* lds, uint32_t lane) {
+    constexpr uint32_t kRowBytes = 8u * (FMT == kKvQ8_0 ? 34u : 18u);
+    uint8_t* const rows[2] = {lds, lds + kRowBytes};
+    const uint32_t blk[2] = {lane / 8u, lane / 8u};
+    encode_items<FMT, 2, NORM>(x, inv, bmax, rows, blk, lane & 7u);
+}
+
+// Two encoded rows side by side in LDS at `lds` (2 x 17 / 2 x 9 16-byte
+// chunks, one per lane): store them (a row whose `ok` is false stores
+// nothing) and return the store's address and data.  The hardware reads a
+// vector store's registers after issue, so the compiler makes the first
+// instruction that overwrites them wait for every outstanding vector memory
+// operation; a caller that keeps them alive (keep_alive) until its end
+// leaves that wait out.  The caller hands the LDS over first.
+struct PendingStore {
+    global_f32x4* addr;
+    f32x4 data;
+};
+
+template <int FMT>
+__device__ __forceinline__ PendingStore flush_rows2(const uint8_t* lds, uint8_t* const (&dst)[2], const bool (&ok)[2],
+                                                    uint32_t lane) {
+    constexpr uint32_t n16 = 8u * (FMT == kKvQ8_0 ? 34u : 18u) / 16u;
+    const uint32_t r = lane >= n16 ? 1u : 0u, c = lane - r * n16;
+    PendingStore st;
+    st.addr = (global_f32x4*)(r ? dst[1] : dst[0]) + c;
+    st.data = reinterpret_cast<const f32x4*>(lds)[min(lane, 2 * n16 - 1)];
+    if (lane < 2 * n16 && (r ? ok[1] : ok[0])) __builtin_nontemporal_store(st.data, st.addr);
+    return st;
+}
+
+__device__ __forceinline__ void keep_alive(const PendingStore& st) {
+    __asm__ volatile("" ::"v"(st.addr), "v"(st.data));
 }
 
 template <int FMT, bool VNORM, int V4>
@@ -300,14 +484,16 @@ __global__ __launch_bounds__(256) void kv_append_row_kernel(KvAppendArgs a) {
     const bool is_v = (wave & 1u) != 0;
     const uint32_t t = blockIdx.x * 2 + (wave >> 1);
     if (t >= a.tokens) return;
-    // the row's loads go out before the position's round trip returns (a
-    // skipped position only discards them)
+    // the position's load goes out first and the row's right behind it (a
+    // skipped position only discards them): loads return in issue order,
+    // so the position is waited for alone
+    const uint32_t position = a.positions[t];
+    __asm__ volatile("" ::: "memory");
     const f32x4* src = reinterpret_cast<const f32x4*>((is_v ? a.value : a.key) + static_cast<size_t>(t) * kW);
     f32x4 x[V4];
 #pragma unroll
     for (int i = 0; i < V4; ++i) x[i] = __builtin_nontemporal_load(src + lane + 64u * i);
     __asm__ volatile("" ::: "memory");  // keeps the loads above the position test
-    const uint32_t position = a.positions[t];
     if (position >= a.capacity) return;
     uint8_t* dst = a.cache + (static_cast<size_t>(is_v ? a.capacity : 0u) + position) * kRowBytes;
     if (VNORM && is_v) {
@@ -329,57 +515,95 @@ __global__ __launch_bounds__(256) void kv_append_row_kernel(KvAppendArgs a) {
 }
 
 // V-norm appends of many tokens at kv_width 256: eight tokens per
-// workgroup, two per wavefront.  Lanes 0..7 of wavefront 0 fold the eight V
-// rows' squares in index order in one instruction stream (each lane's fold
-// is the per-token kernel's, so the bits are the same) while every
-// wavefront encodes and stores its K rows; the V rows are scaled and encoded
-// once their inverse RMS is published.  A token at a position past the
-// capacity (or past the last token) stores nothing.
+// workgroup, two per wavefront, and a fifth wavefront whose lanes 0..7 fold
+// the eight V rows' squares in index order in one instruction stream (each
+// lane's fold is the per-token kernel's, so the bits are the same) while
+// the four others encode and store their K rows and take their V rows'
+// block maxima; the V rows are scaled and encoded once their inverse RMS is
+// published.  A token at a position past the capacity (or past the last
+// token) stores nothing.
+constexpr uint32_t kRows8Threads = 5 * kWave;
+
 template <int FMT>
-__global__ __launch_bounds__(256) void kv_append_rows8_kernel(KvAppendArgs a) {
+__global__ __launch_bounds__(kRows8Threads) void kv_append_rows8_kernel(KvAppendArgs a) {
     constexpr uint32_t kW = 256;
     constexpr uint32_t kRowBytes = FMT == kKvF32 ? kW * 4 : (kW / 32) * (FMT == kKvQ8_0 ? 34u : 18u);
     // V squares, one row per token; a 65-float4 stride puts the eight rows
     // that lanes 0..7 read together on distinct LDS banks
     __shared__ __align__(16) f32x4 sq[8][65];
     __shared__ float inv_lds[8];
-    __shared__ __align__(16) uint8_t rowbuf[4][FMT == kKvF32 ? 16 : kRowBytes];
+    __shared__ __align__(16) uint8_t rowbuf[4][FMT == kKvF32 ? 16 : 4 * kRowBytes];  // K0 K1 V0 V1
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
-    const uint32_t tb = blockIdx.x * 8u + 2u * wave;  // this wavefront's tokens tb, tb + 1
-    f32x4 k[2][1], v[2][1];
+    const bool folder = wave == 4;
+    const uint32_t tb = blockIdx.x * 8u + 2u * (folder ? 0u : wave);  // this wavefront's tokens tb, tb + 1
+    f32x4 k[2], v[2];
+    bool ok[2] = {false, false};
+    uint8_t* kdst[2];
+    uint8_t* vdst[2];
+    if (!folder) {
+        // Vector loads return in issue order, so a wait for one load waits
+        // for every load issued before it.  Issue order: the two positions
+        // (needed first, for the store addresses), the V rows (the fold
+        // waits only for them), then the K rows, which arrive while the
+        // fold runs.
+        uint32_t position[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const size_t t = min(tb + i, a.tokens - 1);  // loads of a token past the end are clamped, never stored
-        k[i][0] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a.key + t * kW) + lane);
-        v[i][0] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a.value + t * kW) + lane);
-    }
-    __asm__ volatile("" ::: "memory");  // keeps the loads above the position reads
-    uint32_t position[2];
+        for (int i = 0; i < 2; ++i) position[i] = a.positions[min(tb + i, a.tokens - 1)];
+        __asm__ volatile("" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 2; ++i) position[i] = tb + i < a.tokens ? a.positions[tb + i] : a.capacity;
+        for (int i = 0; i < 2; ++i) {
+            const size_t t = min(tb + i, a.tokens - 1);  // loads of a token past the end are clamped, never stored
+            v[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a.value + t * kW) + lane);
+        }
+        __asm__ volatile("" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const f32x4 x = v[i][0];
-        sq[2 * wave + i][lane] = f32x4{x.x * x.x, x.y * x.y, x.z * x.z, x.w * x.w};
+        for (int i = 0; i < 2; ++i) {
+            const size_t t = min(tb + i, a.tokens - 1);
+            k[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a.key + t * kW) + lane);
+        }
+        __asm__ volatile("" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            ok[i] = tb + i < a.tokens && position[i] < a.capacity;
+            const uint32_t p = ok[i] ? position[i] : 0u;  // no address is formed past the cache
+            kdst[i] = a.cache + static_cast<size_t>(p) * kRowBytes;
+            vdst[i] = a.cache + (static_cast<size_t>(a.capacity) + p) * kRowBytes;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            sq[2 * wave + i][lane] = f32x4{v[i].x * v[i].x, v[i].y * v[i].y, v[i].z * v[i].z, v[i].w * v[i].w};
     }
     __syncthreads();
-    if (wave == 0 && lane < 8) inv_lds[lane] = inverse_rms(fold_lds_chunk(sq[lane], 64u, 0.0f), static_cast<float>(kW),
-                                                           a.epsilon);
+    float vmax[2] = {0.0f, 0.0f};
+    PendingStore kstore;
+    if (folder) {
+        if (lane < 8)
+            inv_lds[lane] = inverse_rms(fold_lds_chunk(sq[lane], 64u, 0.0f), static_cast<float>(kW), a.epsilon);
+    } else if (FMT == kKvF32) {
+        const float one[2] = {1.0f, 1.0f};
+        store_f32_rows2<false>(k, one, kdst, ok, lane);
+    } else {
+        // while the fold runs: the K rows are encoded and stored (their
+        // writes overlap the fold), and the V rows' block maxima are taken
+        const float one[2] = {1.0f, 1.0f};
+        const float kmax[2] = {block_max(k[0]), block_max(k[1])};
+        encode_rows2<FMT, false>(k, one, kmax, rowbuf[wave], lane);
+        lds_wave_handoff();
+        kstore = flush_rows2<FMT>(rowbuf[wave], kdst, ok, lane);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-        if (position[i] < a.capacity)
-            store_row<FMT, 1>(k[i], a.cache + static_cast<size_t>(position[i]) * kRowBytes, rowbuf[wave], lane,
-                              kRowBytes);
+        for (int i = 0; i < 2; ++i) vmax[i] = block_max(v[i]);
+    }
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        if (position[i] >= a.capacity) continue;
-        const float inv = inv_lds[2 * wave + i];
-        const f32x4 x = v[i][0];
-        const f32x4 y[1] = {f32x4{x.x * inv, x.y * inv, x.z * inv, x.w * inv}};
-        store_row<FMT, 1>(y, a.cache + (static_cast<size_t>(a.capacity) + position[i]) * kRowBytes, rowbuf[wave],
-                          lane, kRowBytes);
+    if (folder) return;
+    const float inv[2] = {inv_lds[2 * wave], inv_lds[2 * wave + 1]};
+    if (FMT == kKvF32) {
+        store_f32_rows2<true>(v, inv, vdst, ok, lane);
+    } else {
+        encode_rows2<FMT, true>(v, inv, vmax, rowbuf[wave] + 2 * kRowBytes, lane);
+        lds_wave_handoff();
+        flush_rows2<FMT>(rowbuf[wave] + 2 * kRowBytes, vdst, ok, lane);
+        keep_alive(kstore);
     }
 }
 
@@ -391,7 +615,7 @@ bool launch_row(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
     if ((w != 256 && w != 512 && w != 1024) || !aligned16(a.key) || !aligned16(a.value) || !aligned16(a.cache))
         return false;
     if (vnorm && w == 256 && a.tokens >= 256) {
-        hipLaunchKernelGGL((kv_append_rows8_kernel<FMT>), dim3((a.tokens + 7) / 8), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((kv_append_rows8_kernel<FMT>), dim3((a.tokens + 7) / 8), dim3(kRows8Threads), 0, stream, a);
         return true;
     }
     const dim3 grid((a.tokens + 1) / 2);

@@ -75,19 +75,32 @@ def _values(r, tokens, w, kind):
         v[1::4, 5] = nan                                     # one NaN: with the V norm the whole row is NaN
         v[2::4] = nan                                        # an all-NaN row
         v[3::4, ::3] = nan                                   # NaN beside finite values in every block
+    elif kind == "band":
+        # quotients on, just inside and just outside the row engine's band of
+        # 2^-12 around half-integers (where it recomputes with a division):
+        # even rows open every block with -8 (Q4_0 scale 1), odd rows with 127
+        # (Q8_0 scale 1), so value = quotient
+        offs = np.array([0.0, 2.0 ** -13, -2.0 ** -13, 2.0 ** -11, -2.0 ** -11, 2.0 ** -20, -2.0 ** -20, 0.25])
+        idx = np.arange(tokens * w).reshape(tokens, w)
+        half = r.integers(-8, 8, (tokens, w)) + 0.5
+        half[1::2] = r.integers(-126, 126, (len(half[1::2]), w)) + 0.5
+        v = (half + offs[idx % 8]).astype(f32)
+        v[0::2, ::32] = f32(-8.0)
+        v[1::2, ::32] = f32(127.0)
     return v
 
 
 @pytest.mark.parametrize("fmt", ["f32", "q8_0", "q4_0"])
 @pytest.mark.parametrize("w,tokens,cap", [(256, 1, 64), (512, 1, 4096), (256, 4096, 4096), (256, 301, 512),
                                           (32, 9, 16), (4096, 3, 4), (96, 33, 40), (1024, 130, 128)])
-@pytest.mark.parametrize("kind", ["normal", "adversarial", "nan"])
+@pytest.mark.parametrize("kind", ["normal", "adversarial", "nan", "band"])
 def test_kv_append_shapes(rt, ora, fmt, w, tokens, cap, kind):
     """Decode (one token at a random position), prefill batches (eight tokens
     per workgroup with the V norm at width 256, a ragged last workgroup at
     301 tokens), ragged widths,
-    positions past the capacity (skipped), adversarial blocks, and NaN blocks
-    and rows (the encoders' maximum starts at 0, as the reference's does)."""
+    positions past the capacity (skipped), adversarial blocks, NaN blocks
+    and rows (the encoders' maximum starts at 0, as the reference's does),
+    and quotients at and beside half-integers (the exact recompute)."""
     r = np.random.default_rng(w * 7 + tokens + cap)
     key, value = _values(r, tokens, w, kind), _values(r, tokens, w, kind)
     pos = r.permutation(max(cap, tokens))[:tokens].astype(np.uint32) if tokens > 1 else \
