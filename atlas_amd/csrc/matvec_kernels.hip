@@ -121,7 +121,11 @@ __device__ __forceinline__ float q4_block_dot(const uint32_t (&q)[4], const floa
     float acc = 0.0f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-        const uint32_t lo = q[w] & 0x0f0f0f0fu, hi = (q[w] >> 4) & 0x0f0f0f0fu;
+        uint32_t lo = q[w] & 0x0f0f0f0fu, hi = (q[w] >> 4) & 0x0f0f0f0fu;
+        // hide the masks' known-zero bits: knowing them, the compiler extracts
+        // each nibble with a bitfield extract before a byte-0 conversion
+        // (two instructions) instead of converting byte k directly (one)
+        __asm__("" : "+v"(lo), "+v"(hi));
 #pragma unroll
         for (int k = 0; k < 4; ++k) {  // byte-wise conversions (v_cvt_f32_ubyte0..3)
             acc = __builtin_fmaf(static_cast<float>((lo >> (8 * k)) & 0xffu), y[4 * w + k], acc);
@@ -228,8 +232,15 @@ __global__ __launch_bounds__(256) void q4_0_matvec_kernel(MatvecArgs a) {
         dst[min(lane + 3 * kWave, n16 - 1)] = w3;
     }
     __syncthreads();
+    // The projection is held to a tolerance (this kernel's own summation
+    // order), so the inverse RMS takes the hardware reciprocal and reciprocal
+    // square root (each within 1 ulp): rsq(sum * rcp(n) + eps), a few ulp,
+    // where the IEEE form (two divisions and a square root) costs ~45
+    // instructions per wavefront.
     float inv = 1.0f;
-    if (rms) inv = inverse_rms((partial[0] + partial[1]) + (partial[2] + partial[3]), static_cast<float>(n), a.epsilon);
+    if (rms)
+        inv = __builtin_amdgcn_rsqf(((partial[0] + partial[1]) + (partial[2] + partial[3])) *
+                                        __builtin_amdgcn_rcpf(static_cast<float>(n)) + a.epsilon);
 
     // 4. lane (g, s): row wrow0 + g, blocks s + LPR * i
     const uint32_t row = wrow0 + g;
