@@ -116,6 +116,7 @@ SIGNATURES = {
     "atlas_hip_matmul_q4_0_qkv_rms_f32": [CTX, P, P, P, P, P, P, P, U32, U32, U32, P, F],
     "atlas_hip_matmul_q4_0_gate_up_rms_f32": [CTX, P, P, P, P, P, U32, U32, P, F],
     "atlas_hip_ple_gate_gelu_f32": [CTX, P, P, P, U32, P, U32, U32],
+    "atlas_hip_ple_projection_f16": [CTX, P, P, P, P, U32, U32, U32, F, F],
     "atlas_hip_kv_append_f32": [CTX, P, P, P, U32, U32, P, U32, c_int, F],
     "atlas_hip_kv_append_q8_0": [CTX, P, P, P, U32, U32, P, U32, c_int, F],
     "atlas_hip_kv_append_q4_0": [CTX, P, P, P, U32, U32, P, U32, c_int, F],

@@ -762,6 +762,26 @@ int atlas_hip_ple_gate_gelu_f32(atlas_hip_ctx* ctx, const float* input, const ui
     return q4_matvec(ctx, input, nullptr, 0.0f, input_width, 1, w, o, n, "ple_gate_gelu", ple, ple_offset);
 }
 
+int atlas_hip_ple_projection_f16(atlas_hip_ctx* ctx, const float* input, const uint16_t* weights,
+                                 const float* norm_weight, float* output, uint32_t hidden, uint32_t width,
+                                 uint32_t groups, float scale, float epsilon) {
+    int rc = enter(ctx);
+    if (rc) return rc;
+    if (!input || !weights || !norm_weight || !output) return invalid(ctx, "PLE projection buffer is null");
+    if (hidden == 0 || hidden % 8 != 0 || hidden > atlas::ple_projection_max_hidden())
+        return invalid(ctx, "PLE projection hidden must be a positive multiple of 8, at most 4096");
+    if (width == 0 || width % 16 != 0 || width > 1024)
+        return invalid(ctx, "PLE projection width must be a positive multiple of 16, at most 1024");
+    if (groups == 0 || groups > atlas::ple_projection_max_groups())
+        return invalid(ctx, "PLE projection groups must be between 1 and 1024");
+    if (!aligned16(input) || !aligned16(weights))
+        return invalid(ctx, "PLE projection input and weights must be 16-byte aligned");
+    if (!std::isfinite(scale)) return invalid(ctx, "PLE projection scale must be finite");
+    if (!finite_positive(epsilon)) return invalid(ctx, "epsilon must be finite and positive");
+    atlas::PleProjArgs a{input, weights, norm_weight, output, hidden, width, groups, scale, epsilon};
+    return launched(ctx, atlas::launch_ple_projection_f16(ctx->stream, a), "ple_projection_f16");
+}
+
 int atlas_hip_matvec_q4_0_rms_f32(atlas_hip_ctx* ctx, const float* input, const uint8_t* weights, float* output,
                                   uint32_t input_width, uint32_t output_width, const float* rms_weight,
                                   float epsilon) {

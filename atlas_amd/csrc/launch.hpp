@@ -123,6 +123,24 @@ struct MatvecArgs {
 uint32_t q4_0_matvec_max_input();
 hipError_t launch_q4_0_matvec(hipStream_t stream, MatvecArgs a);
 
+// The PLE projection of one decode token and its norm (matvec_kernels.hip,
+// then the stable group norm of norm_kernels.hip in place):
+// out = stable_group_rms_norm(scale * (W . input)), W [groups * width, hidden] F16.
+struct PleProjArgs {
+    const float* input;        // [hidden], 16-byte aligned
+    const uint16_t* weights;   // [groups * width, hidden] F16 bits, 16-byte aligned
+    const float* norm_weight;  // [width]
+    float* output;             // [groups * width]
+    uint32_t hidden;           // multiple of 8, <= ple_projection_max_hidden()
+    uint32_t width;            // multiple of 16, <= 1024
+    uint32_t groups;           // <= ple_projection_max_groups()
+    float scale;
+    float epsilon;
+};
+uint32_t ple_projection_max_hidden();
+uint32_t ple_projection_max_groups();
+hipError_t launch_ple_projection_f16(hipStream_t stream, const PleProjArgs& a);
+
 // KV-cache append with optional fused V RMSNorm (kv_kernels.hip).
 enum KvFormat : int { kKvF32 = 0, kKvQ8_0 = 1, kKvQ4_0 = 2 };
 struct KvAppendArgs {

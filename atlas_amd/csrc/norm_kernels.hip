@@ -807,6 +807,67 @@ __global__ __launch_bounds__(64) void groups_stable_kernel(float* values, const 
     for (uint32_t i = lane; i < width; i += kWave) v[i] = v[i] * inv * weight[i];
 }
 
+// Groups of width <= 64 * PER: the same steps with the group and its norm
+// weights held in registers (lane l: values l + 64k), one read and one write
+// of global memory; the sequential fold stages the squares in LDS as above.
+template <int PER>
+__global__ __launch_bounds__(64) void groups_stable_reg_kernel(float* values, const float* weight, uint32_t width,
+                                                               float epsilon, int sequential) {
+    __shared__ __align__(16) float sq[64 * PER];
+    const uint32_t lane = threadIdx.x;
+    float* v = values + static_cast<size_t>(blockIdx.x) * width;
+    float x[PER], w[PER];
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const uint32_t i = lane + kWave * k;
+        x[k] = i < width ? v[i] : 0.0f;
+        w[k] = i < width ? weight[i] : 0.0f;
+        m = fmaxf(m, fabsf(x[k]));
+    }
+    m = wave_max(m);
+    if (m == 0.0f) {
+#pragma unroll
+        for (int k = 0; k < PER; ++k)
+            if (lane + kWave * k < width) v[lane + kWave * k] = 0.0f;
+        return;
+    }
+    float partial = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const uint32_t i = lane + kWave * k;
+        const float scaled = fdiv_rn(x[k], m);
+        const float s2 = scaled * scaled;
+        if (sequential) {
+            if (i < width) sq[i] = s2;
+        } else if (i < width) {
+            partial = partial + s2;
+        }
+    }
+    float sum;
+    if (sequential) {
+        __syncthreads();
+        __shared__ float total;
+        if (lane == 0) {
+            float s = 0.0f;
+            if (width % 4 == 0)
+                s = fold_lds_chunk(reinterpret_cast<const f32x4*>(sq), width / 4, 0.0f);
+            else
+                for (uint32_t i = 0; i < width; ++i) s = s + sq[i];
+            total = s;
+        }
+        __syncthreads();
+        sum = total;
+    } else {
+        sum = wave_sum(partial);
+    }
+    const float root = sqrt_rn(fdiv_rn(sum, static_cast<float>(width)) + fdiv_rn(epsilon, m * m));
+    const float inv = fdiv_rn(fdiv_rn(1.0f, root), m);
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+        if (lane + kWave * k < width) v[lane + kWave * k] = x[k] * inv * w[k];
+}
+
 // ---------------------------------------------------------------------------
 // FP16-storage RMSNorm (optionally fused with the pre-norm residual add).
 // Storage f16, math f32: widening is exact, outputs are rounded RNE.  With a
@@ -1198,6 +1259,19 @@ hipError_t launch_rms_norm_groups_stable_f32(hipStream_t stream, Reduction red, 
     // kAuto keeps the sequential fold: one wavefront per 256-wide group folds
     // its squares in order from LDS at no measurable cost
     const bool seq = red != kWide;
+    if (width <= 64 * 16) {
+        const int q = seq ? 1 : 0;
+        if (width <= 64 * 4)
+            hipLaunchKernelGGL((groups_stable_reg_kernel<4>), dim3(groups), dim3(kWave), 0, stream, values, weight,
+                               width, epsilon, q);
+        else if (width <= 64 * 8)
+            hipLaunchKernelGGL((groups_stable_reg_kernel<8>), dim3(groups), dim3(kWave), 0, stream, values, weight,
+                               width, epsilon, q);
+        else
+            hipLaunchKernelGGL((groups_stable_reg_kernel<16>), dim3(groups), dim3(kWave), 0, stream, values, weight,
+                               width, epsilon, q);
+        return hipGetLastError();
+    }
     const size_t lds = seq ? static_cast<size_t>(width) * sizeof(float) : 0;
     hipLaunchKernelGGL(groups_stable_kernel, dim3(groups), dim3(kWave), lds, stream, values, weight,
                        width, groups, epsilon, seq ? 1 : 0);

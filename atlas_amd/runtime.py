@@ -293,6 +293,13 @@ class HipRuntime:
         self._check(self.lib.atlas_hip_ple_gate_gelu_f32(self.ctx, _ptr(x), _ptr(weights), _ptr(ple), ple_offset,
                                                          _ptr(out), input_width, output_width))
 
+    # The PLE projection of one decode token with its stable group norm as
+    # epilogue (matvec_f16 + scalar_multiply_f32 + rms_norm_groups_in_place_stable_f32,
+    # kernels.metal:731-740, 897-917; gemma4_executor.rs:4184-4214); weights are F16 bits.
+    def ple_projection_f16(self, x, weights, norm_weight, out, hidden, width, groups, scale, eps):
+        self._check(self.lib.atlas_hip_ple_projection_f16(self.ctx, _ptr(x), _ptr(weights), _ptr(norm_weight),
+                                                          _ptr(out), hidden, width, groups, scale, eps))
+
     # KV-cache append with the fused V RMSNorm (kv_append_decode_*[_batch|_vnorm],
     # kernels.metal:1197-1436); fmt is "f32", "q8_0" or "q4_0".
     def kv_append(self, fmt, key, value, cache, kv_width, capacity, positions, tokens, vnorm, eps):

@@ -176,7 +176,8 @@ class ConfigOps(Ops):
     """Per-op timing at the other op configurations (separate lines, not the headline):
     c1 = BASELINE configs[0] (SmolLM2-135M-shaped FP32 ops, T=128),
     c2 = BASELINE configs[1] (SmolLM2-1.7B-shaped FP16 storage, T=2048),
-    gemv = the RMS-folded Q4_0 decode projections and the PLE input gate of one Gemma-4-E2B-like token,
+    gemv = the RMS-folded Q4_0 decode projections, the PLE input gate and the normed F16 PLE projection of one
+           Gemma-4-E2B-like token,
     kv = the KV append with the fused V RMSNorm (prefill batch and one decode token),
     logits = the soft cap + greedy argmax decode tail (256 sequences and one token)."""
 
@@ -215,7 +216,9 @@ class ConfigOps(Ops):
             self.host = {"x": wl.normal(r, H), "w": wl.normal(r, H, 1.0, 0.1), "qw": wl.q4_0_table(r, QN, H),
                          "kw": wl.q4_0_table(r, KVN, H), "vw": wl.q4_0_table(r, KVN, H),
                          "gw": wl.q4_0_table(r, F, H), "uw": wl.q4_0_table(r, F, H),
-                         "pgw": wl.q4_0_table(r, PW, H), "ple": wl.normal(r, PL * PW)}
+                         "pgw": wl.q4_0_table(r, PW, H), "ple": wl.normal(r, PL * PW),
+                         "ppw": wl.normal(r, PL * PW * H, 0.0, 0.05).astype(np.float16).view(np.uint16),
+                         "pnw": wl.normal(r, PW, 1.0, 0.1)}
             eps = L.eps
             self.table = {
                 "qkv_rms": (["x", "w", "qw", "kw", "vw"], {"qo": QN, "ko": KVN, "vo": KVN},
@@ -229,6 +232,12 @@ class ConfigOps(Ops):
                 "ple_gate_gelu": (["x", "pgw", "ple"], {"pgo": PW}, PW * rb + H * 4 + PW * 4 + PW * 4,
                                   lambda rt, s: rt.ple_gate_gelu(s["x"], s["pgw"], s["ple"], 17 * PW, s["pgo"], H,
                                                                  PW)),
+                # ... and the PLE projection it follows: F16 [35 * 256, 1536] times the token's state,
+                # the projection scale, the stable group norm as epilogue
+                "ple_projection_f16": (["x", "ppw", "pnw"], {"ppo": PL * PW},
+                                       PL * PW * H * 2 + H * 4 + PW * 4 + PL * PW * 4,
+                                       lambda rt, s: rt.ple_projection_f16(s["x"], s["ppw"], s["pnw"], s["ppo"], H,
+                                                                           PW, PL, H ** -0.5, eps)),
             }
         elif cfg == "kv":
             # KV append with the fused V RMSNorm at the

@@ -339,6 +339,24 @@ int atlas_hip_ple_gate_gelu_f32(atlas_hip_ctx *ctx, const float *input, const ui
                                 const float *ple, uint32_t ple_offset, float *output, uint32_t input_width,
                                 uint32_t output_width);
 
+/* The PLE projection of one decode token with its norm, in one call:
+ * matvec_f16 (kernels.metal:731-740), scalar_multiply_f32 by `scale`, then
+ * rms_norm_groups_in_place_stable_f32 (kernels.metal:897-917) over `groups`
+ * groups of `width` values; callers gemma4_executor.rs:4184-4214 (the
+ * decode PLE chain: ple_projection, its scale, ple_norm).
+ *   p[o]   = (sum_k input[k] * W[o, k]) * scale,  o < groups * width
+ *   out[g] = stable_rms_norm(p[g * width .. (g + 1) * width), norm_weight)
+ * W is F16 [groups * width, hidden] (row o contiguous, the GGUF layout of
+ * per_layer_model_proj); hidden % 8 == 0 and <= 4096, width % 16 == 0 and
+ * <= 1024, groups <= 1024; input and W 16-byte aligned.  Like the
+ * reference's matvec_f16 the dot is floating point (tolerance parity); the
+ * norm follows the reference's steps on the dots (its sum of squares in a
+ * fixed tree order).  Two launches on the context's stream: the scaled
+ * dots into `output`, then the norm in place. */
+int atlas_hip_ple_projection_f16(atlas_hip_ctx *ctx, const float *input, const uint16_t *weights,
+                                 const float *norm_weight, float *output, uint32_t hidden, uint32_t width,
+                                 uint32_t groups, float scale, float epsilon);
+
 /* ---- KV-cache append with the fused V RMSNorm and Q8_0/Q4_0 encoders ----- */
 
 /* kv_append_decode_{f32,q8_0,q4_0}[_batch|_vnorm] (kernels.metal:1197-1436;

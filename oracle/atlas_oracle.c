@@ -297,6 +297,24 @@ void oracle_rms_norm_groups_stable_f32(float *values, const float *weight, size_
     }
 }
 
+/* The decode PLE chain's projection (gemma4_executor.rs:4184-4214):
+ * matvec_f16 (kernels.metal:731-740: one row at a time, sum += input[k] *
+ * float(W[o, k]) in column order), scalar_multiply_f32 by `scale`, then
+ * rms_norm_groups_in_place_stable_f32 over `groups` groups of `width`. */
+void oracle_ple_projection_f16(const float *input, const uint16_t *weights, const float *norm_weight,
+                               float *output, size_t hidden, size_t width, size_t groups, float scale,
+                               float epsilon) {
+    for (size_t o = 0; o < groups * width; ++o) {
+        float sum = 0.0f;
+        for (size_t k = 0; k < hidden; ++k) {
+            const float product = input[k] * oracle_f16_to_f32(weights[o * hidden + k]);
+            sum = sum + product;
+        }
+        output[o] = sum * scale;
+    }
+    oracle_rms_norm_groups_stable_f32(output, norm_weight, width, groups, epsilon);
+}
+
 /* FP16-storage RMSNorm (config C2): exact widening, FP32 math as
  * oracle_rms_norm_f32, output rounded RNE to f16. */
 void oracle_rms_norm_f16(const uint16_t *input, const uint16_t *weight, uint16_t *output,

@@ -75,6 +75,11 @@ void oracle_rms_norm_add_scale_f32(const float *input, const float *weight,
 void oracle_rms_norm_groups_stable_f32(float *values, const float *weight,
                                        size_t width, size_t groups,
                                        float epsilon);
+/* matvec_f16 (kernels.metal:731-740) * scale, then the stable group norm:
+ * the decode PLE projection (gemma4_executor.rs:4184-4214). */
+void oracle_ple_projection_f16(const float *input, const uint16_t *weights, const float *norm_weight,
+                               float *output, size_t hidden, size_t width, size_t groups, float scale,
+                               float epsilon);
 void oracle_rms_norm_f16(const uint16_t *input, const uint16_t *weight,
                          uint16_t *output, size_t rows, size_t hidden,
                          float epsilon);

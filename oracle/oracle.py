@@ -34,6 +34,7 @@ _SIGS = {
     "oracle_add_rms_norm_f32": ([P, P, P, P, P, SZ, SZ, F], None),
     "oracle_rms_norm_add_scale_f32": ([P, P, P, F, SZ, SZ, F], None),
     "oracle_rms_norm_groups_stable_f32": ([P, P, SZ, SZ, F], None),
+    "oracle_ple_projection_f16": ([P, P, P, P, SZ, SZ, SZ, F, F], None),
     "oracle_rms_norm_f16": ([P, P, P, SZ, SZ, F], None),
     "oracle_add_rms_norm_f16": ([P, P, P, P, P, SZ, SZ, F], None),
     "oracle_gemma4_rope_angle": ([SZ, SZ, SZ, F, F], c_float),
@@ -154,6 +155,14 @@ def rms_norm_groups_stable(values, w, width, groups, eps):
     w = _c(w, f32)
     lib().oracle_rms_norm_groups_stable_f32(_p(v), _p(w), width, groups, eps)
     return v
+
+
+def ple_projection_f16(x, weights, norm_weight, hidden, width, groups, scale, eps):
+    """matvec_f16 * scale, then the stable group norm (gemma4_executor.rs:4184-4214)."""
+    x, weights, nw = _c(x, f32), _c(weights, u16), _c(norm_weight, f32)
+    out = np.empty(groups * width, f32)
+    lib().oracle_ple_projection_f16(_p(x), _p(weights), _p(nw), _p(out), hidden, width, groups, scale, eps)
+    return out
 
 
 def rms_norm_f16(x, w, rows, hidden, eps):

@@ -208,3 +208,116 @@ def test_ple_gate_invalid_input(rt):
         with pytest.raises(OperatorError) as e:
             bad()
         assert e.value.kind == "InvalidInput"
+
+
+# ---- the PLE projection with its stable group norm (matvec_f16 + scale +
+# rms_norm_groups_in_place_stable_f32, kernels.metal:731-740, 897-917;
+# gemma4_executor.rs:4184-4214) ----------------------------------------------
+
+def _ple_projection64(x, W16, nw, hidden, width, groups, scale, eps):
+    """float64 of the same steps: exact dots (numpy matmul), the scale, the
+    stable norm; also mag = |scale| * sum_k |x_k W[o, k]|, the scale of any
+    f32 evaluation's rounding error in the dot."""
+    Wf = W16.view(np.float16).astype(np.float64).reshape(groups * width, hidden)
+    xd = x.astype(np.float64)
+    p = (Wf @ xd) * float(scale)
+    mag = (np.abs(Wf) @ np.abs(xd)) * abs(float(scale))
+    out = np.zeros_like(p)
+    for g in range(groups):
+        v = p[g * width:(g + 1) * width]
+        m = np.max(np.abs(v))
+        if m == 0:
+            continue
+        inv = (1.0 / np.sqrt(np.sum((v / m) ** 2) / width + eps / (m * m))) / m
+        out[g * width:(g + 1) * width] = v * inv * nw.astype(np.float64)
+    return p, mag, out
+
+
+def _check_ple_projection(name, got, p64, mag, out64, width, groups):
+    """Per group: the f32 dots are within TOL * mag of the exact ones, so the
+    normalised group (out = p w / rms(p), scale-free) moves by at most about
+    twice their normwise relative error; plus a few ulp for the norm's own
+    roundings.  An all-zero group is exactly zero."""
+    for g in range(groups):
+        sl = slice(g * width, (g + 1) * width)
+        pn = np.linalg.norm(p64[sl])
+        if pn == 0:
+            assert np.array_equal(got[sl], np.zeros(width, f32)), f"{name} group {g}: zero group not zero"
+            continue
+        kappa = np.linalg.norm(mag[sl]) / pn
+        err = np.linalg.norm(got[sl].astype(np.float64) - out64[sl]) / np.linalg.norm(out64[sl])
+        assert err <= 2 * TOL * kappa + 1e-6, f"{name} group {g}: normwise {err:.3e} (kappa {kappa:.1f})"
+
+
+def _ple_case(r, hidden, width, groups, zero_group=None):
+    x = (0.5 * r.standard_normal(hidden)).astype(f32)
+    W = (0.05 * r.standard_normal((groups * width, hidden))).astype(np.float16)
+    if zero_group is not None:
+        W[zero_group * width:(zero_group + 1) * width] = 0
+    nw = (1.0 + 0.1 * r.standard_normal(width)).astype(f32)
+    return x, W.view(np.uint16).reshape(-1), nw
+
+
+@pytest.mark.parametrize("hidden,width,groups", [(1536, 256, 35), (64, 16, 1), (1000, 32, 5), (4096, 1024, 3),
+                                                 (8, 16, 2), (2560, 128, 9)])
+def test_ple_projection_f16(rt, ora, hidden, width, groups):
+    """Gemma-4-E2B's decode shape (hidden 1536, 35 groups of 256), a width of
+    16 and of 1024, ragged hidden widths (1000: the last 512-column chunk is
+    partial; 8), against float64 and against the f32 restatement; one group
+    all zero; two calls in a row with different inputs."""
+    r = np.random.default_rng(900 + hidden + width + groups)
+    scale = float(hidden) ** -0.5
+    for call in range(2):
+        x, W, nw = _ple_case(r, hidden, width, groups, zero_group=(groups - 1 if groups > 1 else None))
+        say(f"ple projection hidden={hidden} width={width} groups={groups} call {call}")
+        dx, dW, dn, out = rt.upload(x), rt.upload(W), rt.upload(nw), rt.empty(groups * width)
+        rt.ple_projection_f16(dx, dW, dn, out, hidden, width, groups, scale, EPS)
+        rt.sync()
+        got = out.download(groups * width)
+        p64, mag, out64 = _ple_projection64(x, W, nw, hidden, width, groups, scale, EPS)
+        _check_ple_projection(f"call {call}", got, p64, mag, out64, width, groups)
+        ref = ora.ple_projection_f16(x, W, nw, hidden, width, groups, scale, EPS)
+        _check_ple_projection(f"call {call} (oracle)", ref, p64, mag, out64, width, groups)
+
+
+def test_ple_projection_graph_replays(rt):
+    """Captured once (both of its launches), replayed three times with a new
+    input written eagerly before each replay."""
+    hidden, width, groups = 1536, 256, 35
+    r = np.random.default_rng(77)
+    x, W, nw = _ple_case(r, hidden, width, groups)
+    dx, dW, dn, out = rt.upload(x), rt.upload(W), rt.upload(nw), rt.empty(groups * width)
+    scale = hidden ** -0.5
+    rt.graph_begin()
+    try:
+        rt.ple_projection_f16(dx, dW, dn, out, hidden, width, groups, scale, EPS)
+    finally:
+        g = rt.graph_end()
+    try:
+        for i in range(3):
+            xi = (0.5 * r.standard_normal(hidden)).astype(f32)
+            dx.upload(xi)
+            say(f"ple projection graph replay {i}")
+            rt.graph_launch(g)
+            rt.sync()
+            p64, mag, out64 = _ple_projection64(xi, W, nw, hidden, width, groups, scale, EPS)
+            _check_ple_projection(f"replay {i}", out.download(groups * width), p64, mag, out64, width, groups)
+    finally:
+        rt.graph_destroy(g)
+
+
+def test_ple_projection_invalid_input(rt):
+    say("ple projection invalid input")
+    x, W, n, out = rt.empty(1536), rt.empty(1 << 20), rt.empty(256), rt.empty(8960)
+    for bad in (lambda: rt.ple_projection_f16(x, W, n, out, 1000 + 4, 256, 35, 1.0, EPS),   # hidden % 8
+                lambda: rt.ple_projection_f16(x, W, n, out, 8192, 256, 1, 1.0, EPS),        # hidden > 4096
+                lambda: rt.ple_projection_f16(x, W, n, out, 1536, 250, 35, 1.0, EPS),       # width % 16
+                lambda: rt.ple_projection_f16(x, W, n, out, 1536, 2048, 1, 1.0, EPS),       # width > 1024
+                lambda: rt.ple_projection_f16(x, W, n, out, 1536, 256, 0, 1.0, EPS),
+                lambda: rt.ple_projection_f16(x, W, n, out, 1536, 256, 2000, 1.0, EPS),     # groups > 1024
+                lambda: rt.ple_projection_f16(x, W, n, out, 1536, 256, 35, float("nan"), EPS),
+                lambda: rt.ple_projection_f16(x, W, n, out, 1536, 256, 35, 1.0, 0.0),
+                lambda: rt.ple_projection_f16(x, None, n, out, 1536, 256, 35, 1.0, EPS)):
+        with pytest.raises(OperatorError) as e:
+            bad()
+        assert e.value.kind == "InvalidInput"

@@ -258,14 +258,18 @@ def test_geglu_offset_extremes_and_scalar_shapes(rt, ora):
                     [ora.geglu_offset(gate, ple, layer * width, layers * width, width, rows)])
 
 
-def test_groups_stable(rt, ora):
-    r = wl.rng(23)
-    width, groups = 256, 35 * 64
+@pytest.mark.parametrize("width,groups", [(256, 35 * 64), (250, 37), (64, 11), (512, 35), (1024, 9), (1000, 13),
+                                          (2000, 7)])
+def test_groups_stable(rt, ora, width, groups):
+    """Widths held in registers (64, 250: not a multiple of 4, 256, 512,
+    1000, 1024) and the general kernel above 1024; an all-zero group and one
+    of 1e30 (whose squares overflow without the max scaling)."""
+    r = wl.rng(23 + width)
     v = wl.normal(r, (groups, width))
     v[5] = 0.0
-    v[9] *= f32(1e30)
+    v[9 % groups] *= f32(1e30)
     w = wl.normal(r, width, 1, 0.1)
-    say("groups stable")
+    say(f"groups stable width={width} groups={groups}")
     vb = rt.upload(v)
     rt.rms_norm_groups_stable(vb, rt.upload(w), width, groups, 1e-6)
     rt.sync()

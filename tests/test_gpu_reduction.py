@@ -211,3 +211,26 @@ def test_wide_tree_epilogues_normwise(rt_auto, ora):
                 assert np.linalg.norm(got[-1] - exp[-1]) / np.linalg.norm(exp[-1]) <= 1e-6
     finally:
         rt_auto.set_reduction(ATLAS_REDUCTION_AUTO)
+
+
+@pytest.mark.parametrize("width,groups", [(256, 35), (250, 9), (2000, 5)])
+def test_wide_groups_stable(rt_auto, ora, width, groups):
+    """ATLAS_REDUCTION_WIDE sums the stable group norm's squares as a tree
+    (the PLE projection always does): within 1e-6 relative of the
+    sequential oracle per element; an all-zero group stays exactly zero."""
+    r = np.random.default_rng(88 + width)
+    v = r.standard_normal((groups, width)).astype(np.float32)
+    v[1] = 0.0
+    w = (1 + 0.1 * r.standard_normal(width)).astype(np.float32)
+    rt_auto.set_reduction(ATLAS_REDUCTION_WIDE)
+    try:
+        say(f"wide groups stable width={width}")
+        vb = rt_auto.upload(v)
+        rt_auto.rms_norm_groups_stable(vb, rt_auto.upload(w), width, groups, 1e-6)
+        rt_auto.sync()
+        got = vb.download(v.size).reshape(groups, width)
+    finally:
+        rt_auto.set_reduction(ATLAS_REDUCTION_AUTO)
+    exp = ora.rms_norm_groups_stable(v, w, width, groups, 1e-6).reshape(groups, width)
+    assert np.all(got[1] == 0.0)
+    assert np.max(np.abs(got - exp) / np.maximum(np.abs(exp), 1e-30)) <= 1e-6

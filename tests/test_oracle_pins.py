@@ -609,6 +609,54 @@ def test_matvec_q4_0_oracles_pinned(ora):
     np.testing.assert_allclose(got, deq[:, k] * float(c) * float(w[k]) / np.sqrt(9.0 / n + eps), rtol=1e-12)
 
 
+def test_ple_projection_f16_pinned(ora):
+    """The decode PLE projection (matvec_f16 * scale, then the stable group
+    norm; gemma4_executor.rs:4184-4214): against numpy's float64 matmul of the
+    exactly widened F16 weights and the group norm in float64, within the
+    sequential f32 dot's bound carried through the norm; a one-hot input
+    selects one weight column exactly (the dot has no rounding); a zero group
+    stays zero; and a reversed column order (a planted mistake) is caught."""
+    r = np.random.default_rng(41)
+    hidden, width, groups, eps, scale = 96, 32, 4, 1e-6, 0.125
+    x = r.standard_normal(hidden).astype(f32)
+    Wh = (0.1 * r.standard_normal((groups * width, hidden))).astype(np.float16)
+    Wh[width:2 * width] = 0                                   # group 1 all zero
+    W = Wh.view(np.uint16).reshape(-1)
+    nw = (1.0 + 0.1 * r.standard_normal(width)).astype(f32)
+
+    def exact(xv, Wm):
+        p = (Wm.astype(np.float64) @ xv.astype(np.float64)) * scale
+        mag = (np.abs(Wm.astype(np.float64)) @ np.abs(xv.astype(np.float64))) * scale
+        out = np.zeros_like(p)
+        for g in range(groups):
+            v = p[g * width:(g + 1) * width]
+            m = np.max(np.abs(v))
+            if m > 0:
+                out[g * width:(g + 1) * width] = v * ((1 / np.sqrt(np.sum((v / m) ** 2) / width + eps / m / m)) / m) * nw
+        return p, mag, out
+
+    got = ora.ple_projection_f16(x, W, nw, hidden, width, groups, scale, eps)
+    p, mag, out = exact(x, Wh)
+    assert np.all(got[width:2 * width] == 0.0)
+    for g in (0, 2, 3):
+        sl = slice(g * width, (g + 1) * width)
+        # sequential f32 dot: |err| <= (hidden + 2) * 2^-24 * mag; through the
+        # scale-free norm about twice that, normwise, plus the norm's roundings
+        rel = np.linalg.norm(got[sl] - out[sl]) / np.linalg.norm(out[sl])
+        assert rel <= 2 * (hidden + 2) * 2.0 ** -24 * np.linalg.norm(mag[sl]) / np.linalg.norm(p[sl]) + 1e-6
+    # one-hot input: p = scale * W[:, k] exactly, so each group is W[:, k] normalised
+    k = 17
+    e = np.zeros(hidden, f32)
+    e[k] = 1.0
+    got1 = ora.ple_projection_f16(e, W, nw, hidden, width, groups, scale, eps)
+    _, _, out1 = exact(e, Wh)
+    np.testing.assert_allclose(got1, out1, rtol=2e-6, atol=1e-30)
+    # planted mistake: the weights' columns reversed must not pass
+    wrong = ora.ple_projection_f16(x, Wh[:, ::-1].copy().view(np.uint16).reshape(-1), nw, hidden, width, groups,
+                                   scale, eps)
+    assert np.linalg.norm(wrong[:width] - out[:width]) > 0.1 * np.linalg.norm(out[:width])
+
+
 def test_reference_matvec_generators():
     """The restated reference-test generators reproduce the LCG and the weight
     pattern of matvec_rms_fused_parity.rs:16-49."""
