@@ -222,33 +222,36 @@ __global__ __launch_bounds__(64 * WPG) void embed_quant_kernel(const uint8_t* __
 
 // PLE gather-combine, one float4 per thread:
 //   out[t, j] = ((deq(table[id])[j] * embedding_scale) + projection[t, j]) * output_scale
-// Workgroup t * segments + s covers float4 [256 s, 256 s + 256) of token t's row and
-// stages only that segment's table bytes (1024 values: 32 Q4_0 blocks,
-// 576 B, or 4 Q6_K super-blocks, 840 B; the segment starts on a block
-// boundary).  A plain stream with one 16-byte access per thread per operand
-// measured fastest for this read/write mix on MI355X.
-template <bool Q6>
+// Workgroup t * segments + s covers float4 [256 F s, 256 F (s + 1)) of token
+// t's row, thread i the float4 256 F s + 256 f + i (f < F), and stages only
+// that segment's table bytes (1024 F values: 32 F Q4_0 blocks of 18 bytes,
+// or 4 F Q6_K super-blocks of 210; the segment starts on a block boundary).
+template <bool Q6, int F>
 __global__ __launch_bounds__(256) void ple_seg_kernel(const uint8_t* __restrict__ table,
                                                       const uint32_t* __restrict__ ids,
                                                       const float* __restrict__ projection,
                                                       float* __restrict__ out, uint32_t vocab,
                                                       uint32_t row_elems, uint32_t segments,
                                                       float embedding_scale, float output_scale) {
-    __shared__ __align__(16) uint8_t seg[Q6 ? 4 * 210 : 32 * 18];
+    __shared__ __align__(16) uint8_t seg[Q6 ? 4 * F * 210 : 32 * F * 18];
     const uint32_t t = blockIdx.x / segments;
     const uint32_t sg = blockIdx.x - t * segments;
     const uint32_t n4 = row_elems / 4;
-    const uint32_t c4 = 256u * sg + threadIdx.x;
     const size_t base = static_cast<size_t>(t) * row_elems;
-    // no early exit on the id: the projection load stays ahead of the id's
+    // no early exit on the id: the projection loads stay ahead of the id's
     // round trip and the table's (an invalid id stages nothing and skips the
     // store, so its output stays untouched; the id is workgroup-uniform)
-    const f32x4 q = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(projection + base) + min(c4, n4 - 1));
+    f32x4 q[F];
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+        const uint32_t c4 = 256u * (F * sg + f) + threadIdx.x;
+        q[f] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(projection + base) + min(c4, n4 - 1));
+    }
     const uint32_t id_raw = ids[t];
     const bool valid = id_raw < vocab;
     const uint32_t id = valid ? id_raw : 0u;
-    const uint32_t v0 = 1024u * sg;
-    const uint32_t seg_vals = min(1024u, row_elems - v0);
+    const uint32_t v0 = 1024u * F * sg;
+    const uint32_t seg_vals = min(1024u * F, row_elems - v0);
     const uint32_t row_bytes = Q6 ? (row_elems / 256) * 210 : (row_elems / 32) * 18;
     const uint32_t seg_off = Q6 ? (v0 / 256) * 210 : (v0 / 32) * 18;
     const uint32_t seg_bytes = Q6 ? (seg_vals / 256) * 210 : (seg_vals / 32) * 18;
@@ -256,16 +259,20 @@ __global__ __launch_bounds__(256) void ple_seg_kernel(const uint8_t* __restrict_
         stage_row<1, 4, 8>(seg, table + static_cast<size_t>(id) * row_bytes + seg_off, seg_bytes, threadIdx.x,
                            blockDim.x);
     __syncthreads();
-    if (valid && c4 < n4) {
-        float v[4];
-        if (Q6)
-            q6_k_decode4(seg, 4 * c4 - v0, v);
-        else
-            q4_0_decode4(seg, 4 * c4 - v0, v);
-        stg_nt(out + base + 4 * c4, f32x4{(v[0] * embedding_scale + q.x) * output_scale,
-                                          (v[1] * embedding_scale + q.y) * output_scale,
-                                          (v[2] * embedding_scale + q.z) * output_scale,
-                                          (v[3] * embedding_scale + q.w) * output_scale});
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+        const uint32_t c4 = 256u * (F * sg + f) + threadIdx.x;
+        if (valid && c4 < n4) {
+            float v[4];
+            if (Q6)
+                q6_k_decode4(seg, 4 * c4 - v0, v);
+            else
+                q4_0_decode4(seg, 4 * c4 - v0, v);
+            stg_nt(out + base + 4 * c4, f32x4{(v[0] * embedding_scale + q[f].x) * output_scale,
+                                              (v[1] * embedding_scale + q[f].y) * output_scale,
+                                              (v[2] * embedding_scale + q[f].z) * output_scale,
+                                              (v[3] * embedding_scale + q[f].w) * output_scale});
+        }
     }
 }
 
@@ -274,12 +281,17 @@ __global__ __launch_bounds__(256) void ple_seg_kernel(const uint8_t* __restrict_
 template <bool Q6>
 hipError_t launch_ple_it(hipStream_t stream, const uint8_t* table, const uint32_t* ids, const float* projection,
                          float* out, uint32_t vocab, uint32_t row_elems, uint32_t tokens, float es, float os) {
-    const uint32_t segments = (row_elems / 4 + 255) / 256;
+    // two float4 per thread (2048 values per workgroup): the projection
+    // loads of both go out before the id's and the table's round trips.
+    // C4: 48.5 us against 49.8 with one float4 and 49.6 / 49.9 with three /
+    // four (a 8960-value row splits into 4 x 2048 + 768)
+    constexpr int kF = 2;
+    const uint32_t segments = (row_elems / 4 + 256 * kF - 1) / (256 * kF);
     const uint32_t per_launch = 0x7fffffffu / segments;
     for (uint32_t t0 = 0; t0 < tokens; t0 += per_launch) {
         const uint32_t n = min(per_launch, tokens - t0);
         const size_t off = static_cast<size_t>(t0) * row_elems;
-        hipLaunchKernelGGL((ple_seg_kernel<Q6>), dim3(n * segments), dim3(256), 0, stream, table, ids + t0,
+        hipLaunchKernelGGL((ple_seg_kernel<Q6, kF>), dim3(n * segments), dim3(256), 0, stream, table, ids + t0,
                            projection + off, out + off, vocab, row_elems, segments, es, os);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
