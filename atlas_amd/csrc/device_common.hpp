@@ -90,17 +90,43 @@ __device__ __forceinline__ float exp_f32(float x) {
     return x != x ? x : out;
 }
 
+// a / b in four operations instead of the IEEE sequence's ten, for the
+// activations' in-range forms below: q0 = a * rcp(b), the exact residual
+// fma(-q0, b, a), q = fma(residual, rcp(b), q0), and the sign of a (b > 0
+// for every caller, so the quotient's sign is a's; this also keeps -0).
+// Not correctly rounded in general -- v_rcp_f32 is within 1 ulp of 1/b,
+// where Markstein's theorem needs the rounded reciprocal -- but equal to
+// fdiv_rn bit for bit on every operand pair its callers pass: a GPU test
+// (tests/test_gpu_division.py) runs tanh_with, gelu_finite_with and
+// silu_small_with on every binary32 input of their domains with both
+// divisions and finds no difference, and finds differences for the
+// uncorrected product and for the form without the sign step.
+__device__ __forceinline__ float div_inrange(float a, float b) {
+    const float r = __builtin_amdgcn_rcpf(b);
+    const float q0 = a * r;
+    const float q = __builtin_fmaf(__builtin_fmaf(-q0, b, a), r, q0);
+    return __builtin_copysignf(q, a);
+}
+struct DivIeee {
+    __device__ static float div(float a, float b) { return fdiv_rn(a, b); }
+};
+struct DivInRange {
+    __device__ static float div(float a, float b) { return div_inrange(a, b); }
+};
+
 // tanh through its exponential identity with saturation at |x| >= 10
 // (Atlas atlas_tanh_f32, crates/atlas-metal/src/kernels.metal:742-750).
 // Inside (-10, 10), 2v is inside (-20, 20), where exp_small_f32 is exact
 // to exp_f32; outside, the quotient is computed and discarded.  NaN
-// propagates through the quotient.
-__device__ __forceinline__ float tanh_f32(float v) {
+// propagates through the quotient (with DivIeee; DivInRange takes finite v).
+template <class D>
+__device__ __forceinline__ float tanh_with(float v) {
     const float e = exp_small_f32(2.0f * v);
-    const float q = fdiv_rn(e - 1.0f, e + 1.0f);
+    const float q = D::div(e - 1.0f, e + 1.0f);
     // v >= 10 -> 1, v <= -10 -> -1, else q (NaN: the compare fails, q is NaN)
     return __builtin_fabsf(v) >= 10.0f ? __builtin_copysignf(1.0f, v) : q;
 }
+__device__ __forceinline__ float tanh_f32(float v) { return tanh_with<DivIeee>(v); }
 
 // tanh for the logit soft cap, where small arguments must keep their
 // relative accuracy (the (e-1)/(e+1) identity above cancels near 0).  Two
@@ -132,8 +158,11 @@ __device__ __forceinline__ bool tanh_series_range(float a) { return a < 0.625f; 
 // x / (1 + e^-x)   (kernels.metal:27-36)
 __device__ __forceinline__ float silu_f32(float x) { return fdiv_rn(x, 1.0f + exp_f32(-x)); }
 
-// silu_f32 for |x| < 87, where exp_small_f32(-x) == exp_f32(-x).
-__device__ __forceinline__ float silu_small_f32(float x) { return fdiv_rn(x, 1.0f + exp_small_f32(-x)); }
+// silu_f32 for |x| < 87, where exp_small_f32(-x) == exp_f32(-x) and the
+// in-range division gives fdiv_rn's bits.
+template <class D>
+__device__ __forceinline__ float silu_small_with(float x) { return D::div(x, 1.0f + exp_small_f32(-x)); }
+__device__ __forceinline__ float silu_small_f32(float x) { return silu_small_with<DivInRange>(x); }
 
 // SiLU of N values held by each lane.  When every value of the wavefront
 // lies in (-87, 87) -- all ordinary activations -- the straight-line
@@ -156,8 +185,12 @@ __device__ __forceinline__ void silu_lanes(float (&v)[N]) {
 // tanh-GELU with the overflow guard (kernels.metal:752-767):
 // a = c0*(x + ((c1*x)*x)*x); inf(a) -> (a > 0 ? x : 0); else (0.5*x)*(1 + tanh(a)).
 __device__ __forceinline__ float gelu_argument(float x) { return 0.7978845608f * (x + 0.044715f * x * x * x); }
+template <class D>
+__device__ __forceinline__ float gelu_finite_with(float x, float argument) {
+    return 0.5f * x * (1.0f + tanh_with<D>(argument));
+}
 __device__ __forceinline__ float gelu_finite_f32(float x, float argument) {
-    return 0.5f * x * (1.0f + tanh_f32(argument));
+    return gelu_finite_with<DivIeee>(x, argument);
 }
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
     const float argument = gelu_argument(x);
@@ -168,21 +201,22 @@ __device__ __forceinline__ float gelu_tanh_f32(float x) {
 // tanh-GELU of N values held by each lane, with the bits of gelu_tanh_f32.
 // The compiler lowers gelu_tanh_f32's overflow guard to a branch per value,
 // which serialises the N exp/divide chains; here one wave-uniform test
-// replaces it: when no argument of the wavefront is infinite (every
-// |x| < ~1.9e12), the guard selects g for every value, so the straight-line
-// form runs; otherwise the guarded form runs for the whole wavefront.
+// replaces it: when every argument of the wavefront is finite (every
+// |x| < ~1.9e12, no NaN), the guard selects g for every value, so the
+// straight-line form with the in-range division runs; otherwise the guarded
+// IEEE form runs for the whole wavefront.
 template <int N>
 __device__ __forceinline__ void gelu_lanes(float (&v)[N]) {
     float argument[N];
-    bool overflow = false;
+    bool special = false;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
         argument[i] = gelu_argument(v[i]);
-        overflow = overflow || __builtin_isinf(argument[i]);
+        special = special || !(__builtin_fabsf(argument[i]) < __builtin_inff());
     }
-    if (__builtin_amdgcn_ballot_w64(overflow) == 0) {
+    if (__builtin_amdgcn_ballot_w64(special) == 0) {
 #pragma unroll
-        for (int i = 0; i < N; ++i) v[i] = gelu_finite_f32(v[i], argument[i]);
+        for (int i = 0; i < N; ++i) v[i] = gelu_finite_with<DivInRange>(v[i], argument[i]);
     } else {
 #pragma unroll
         for (int i = 0; i < N; ++i) v[i] = gelu_tanh_f32(v[i]);

@@ -49,6 +49,15 @@ def test_stream_floor_library_exports():
     assert lib.atlas_floor_kinds() == 3
 
 
+def test_division_check_library_exports():
+    """The test-only enumeration library the GPU division test loads: built
+    and exporting its entry point (no call without a GPU)."""
+    import ctypes
+    path = os.path.join(ROOT, "atlas_amd", "libatlas_division_check.so")
+    assert os.path.exists(path), "run __graft_entry__.build() first"
+    assert hasattr(ctypes.CDLL(path), "atlas_division_check")
+
+
 def test_buffer_sets_carved_from_one_arena():
     """Every op's rotating sets are views into one arena allocation: each
     tensor 4 KiB aligned, tensors and sets disjoint, set 0 uploaded and the
