@@ -206,7 +206,7 @@ class ConfigOps(Ops):
                                lambda rt, s: rt.swiglu_f16(s["gate"], s["up"], s["o"], T * F)),
             }
         elif cfg == "gemv":
-            # SURVEY 8(f) rank 1: the RMS-folded Q4_0 decode projections of one
+            # the RMS-folded Q4_0 decode projections of one
             # Gemma-4-E2B-like token (hidden 1536; Q 8x256, K/V 1x256; FFN 6144)
             L = wl.GemmaLayerShape()
             H, QN, KVN, F = L.hidden, L.q_heads * L.head_dim, L.head_dim, L.ffn
@@ -228,7 +228,7 @@ class ConfigOps(Ops):
                 "gate_up_rms": (["x", "w", "gw", "uw"], {"go": F, "uo": F}, 2 * F * rb + 2 * H * 4 + 2 * F * 4,
                                 lambda rt, s: rt.matmul_q4_0_gate_up_rms(s["x"], s["gw"], s["uw"], s["go"], s["uo"],
                                                                          H, F, s["w"], eps)),
-                # SURVEY 8(f) rank 3: the PLE input gate of one layer (256 rows, layer 17's PLE slice)
+                # the PLE input gate of one layer (256 rows, layer 17's PLE slice)
                 "ple_gate_gelu": (["x", "pgw", "ple"], {"pgo": PW}, PW * rb + H * 4 + PW * 4 + PW * 4,
                                   lambda rt, s: rt.ple_gate_gelu(s["x"], s["pgw"], s["ple"], 17 * PW, s["pgo"], H,
                                                                  PW)),
@@ -240,7 +240,7 @@ class ConfigOps(Ops):
                                                                            PW, PL, H ** -0.5, eps)),
             }
         elif cfg == "kv":
-            # SURVEY 8(f) rank 2: KV append with the fused V RMSNorm at the
+            # KV append with the fused V RMSNorm at the
             # Gemma-4-E2B-like shape (one KV head of 256): a 4096-token prefill
             # batch into a 4096-position cache, and one decode token
             L = wl.GemmaLayerShape()
@@ -263,7 +263,7 @@ class ConfigOps(Ops):
             self.written = {f"kv_append_{fmt}_vnorm_T{T}": 2 * T * rows[fmt] for fmt in ("f32", "q8_0", "q4_0")}
             self.written["kv_append_q4_0_vnorm_decode"] = 2 * rows["q4_0"]
         elif cfg == "logits":
-            # SURVEY 8(f) rank 4: the decode tail, soft cap (30) + greedy argmax
+            # the decode tail, soft cap (30) + greedy argmax
             # over the 262144-entry vocabulary: the C5 batch of 256 sequences
             # (in place, as the reference caps its logits buffer) and one token
             V, cap = wl.QuantGatherShape().vocab, 30.0
@@ -658,7 +658,7 @@ def cpu_baseline(wl, budget_s=1.0, max_threads=16, host=None):
 
 
 # The reference's published decode figures for this path (Apple M2 Max, one
-# sequence, whole model): context only, not comparable
+# sequence, whole model; docs/atlas-metal-phases/README.md:51-54): context only, not comparable
 # hardware or batch.
 M2_MAX_CONTEXT = {
     "qk_norm_rope_ms_per_token": 2.31,      # docs/atlas-metal-phases/next-improvements.md:51-56
@@ -819,7 +819,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every op of this path is row-independent and this build "
-              "produces no multi-GPU figure (DESIGN.md describes how tokens would shard). Run with --gpus 1.",
+              "produces no multi-GPU figure (a batch would shard by token rows with no exchange). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 
