@@ -38,6 +38,11 @@ __host__ __device__ __forceinline__ uint32_t quant_row_bytes(int fmt, uint32_t h
     return fmt == kQuantQ6K ? (hidden / 256) * 210 : (hidden / 32) * (fmt == kQuantQ8_0 ? 34u : 18u);
 }
 
+// LDS bytes per staged row (16-byte slots).
+__host__ __device__ __forceinline__ uint32_t quant_slot_bytes(int fmt, uint32_t hidden) {
+    return (quant_row_bytes(fmt, hidden) + 15) & ~15u;
+}
+
 // Four consecutive Q4_0 values starting at column `col` (col % 4 == 0).
 __device__ __forceinline__ void q4_0_decode4(const uint8_t* row, uint32_t col, float v[4]) {
     const uint32_t blk = (col >> 5) * 18;
@@ -127,11 +132,44 @@ __device__ __forceinline__ void stage_row(uint8_t* dst, const uint8_t* src, uint
         stage_units<K2, uint16_t>(dst, src, bytes / 2, tid, nthreads);
 }
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ void stg_nt(float* p, f32x4 v) {
-    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+// Stage `units` UNIT-byte units of the row behind `rs` into LDS `dst` with
+// the lanes of one wavefront.  Every load is unconditional -- lanes past the row
+// re-read its last unit -- so a pass's K loads carry no exec-mask branches
+// and are all in flight before the first LDS write; units past the row are
+// not written.
+template <int K, int UNIT>
+__device__ __forceinline__ void stage_units_wave(uint8_t* dst, __amdgpu_buffer_rsrc_t rs, uint32_t units,
+                                                 uint32_t lane) {
+    // units >= 1: the first pass needs no entry test, so nothing between the
+    // id and the first row load waits on a branch
+    uint32_t base = 0;
+    do {
+        u32x4_t v[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const uint32_t off = UNIT * min(base + lane + k * kWave, units - 1u);
+            if constexpr (UNIT == 16)
+                v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+            else if constexpr (UNIT == 4)
+                v[k].x = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+            else
+                v[k].x = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const uint32_t i = base + lane + k * kWave;
+            if (i >= units) continue;
+            if constexpr (UNIT == 16)
+                reinterpret_cast<u32x4_t*>(dst)[i] = v[k];
+            else if constexpr (UNIT == 4)
+                reinterpret_cast<uint32_t*>(dst)[i] = v[k].x;
+            else
+                reinterpret_cast<uint16_t*>(dst)[i] = static_cast<uint16_t>(v[k].x);
+        }
+        base += K * kWave;
+    } while (base < units);
 }
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // FP32 gather: one wavefront per token; the id is wave-uniform (scalar load).
 __global__ __launch_bounds__(64) void embed_f32_kernel(const float* __restrict__ table,
@@ -146,10 +184,11 @@ __global__ __launch_bounds__(64) void embed_f32_kernel(const float* __restrict__
     const float* src = table + static_cast<size_t>(valid ? id : 0) * hidden;
     const bool scaled = scale != 1.0f;
     if (vec) {
+        const auto ro = span_rsrc(dst, hidden * 4u);
         for (uint32_t c = lane * 4; c < hidden; c += 4 * kWave) {
             f32x4 v = valid ? *reinterpret_cast<const f32x4*>(src + c) : f32x4{0.f, 0.f, 0.f, 0.f};
             if (scaled) v = f32x4{v.x * scale, v.y * scale, v.z * scale, v.w * scale};
-            stg_nt(dst + c, v);
+            st_span4<kPolicyWriteThrough>(ro, 4u * c, v);
         }
     } else {
         for (uint32_t c = lane; c < hidden; c += kWave) {
@@ -159,14 +198,14 @@ __global__ __launch_bounds__(64) void embed_f32_kernel(const float* __restrict__
     }
 }
 
-// Q4_0 / Q6_K / Q8_0 gather: TPW tokens per wavefront (tokens w and w + G, G = the
-// grid's wavefront count), WPG wavefronts per workgroup.  Each wavefront
-// pulls its packed rows into its own LDS region with the widest coalesced
-// load the row alignment allows, then each lane decodes four consecutive
-// values per step and writes them with one 128-bit nontemporal store.  The
+// Q4_0 / Q6_K / Q8_0 gather: one token per wavefront, WPG wavefronts per
+// workgroup.  The id arrives through a scalar load; the packed row is staged
+// in the wavefront's own LDS slot (stage_row_wave), then each lane decodes
+// four consecutive values
+// per step and writes them with one 128-bit write-through store.  The
 // handoff from the staging lanes to the decoding lanes is a wavefront-scope
 // fence (no workgroup barrier).
-template <int FMT, int TPW, int WPG>
+template <int FMT, int WPG, int UNIT>
 __global__ __launch_bounds__(64 * WPG) void embed_quant_kernel(const uint8_t* __restrict__ table,
                                                                const uint32_t* __restrict__ ids,
                                                                float* __restrict__ out, uint32_t vocab,
@@ -174,24 +213,25 @@ __global__ __launch_bounds__(64 * WPG) void embed_quant_kernel(const uint8_t* __
     extern __shared__ __align__(16) uint8_t lds_rows[];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
-    const uint32_t w0 = blockIdx.x * WPG + wave;
-    const uint32_t G = gridDim.x * WPG;
+    const uint32_t t = blockIdx.x * WPG + wave;
     const uint32_t row_bytes = quant_row_bytes(FMT, hidden);
-    const uint32_t slot = (row_bytes + 15) & ~15u;
-    uint8_t* rows = lds_rows + static_cast<size_t>(wave) * TPW * slot;
-    uint32_t id[TPW];
-    bool take[TPW];
-#pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-        const uint32_t t = w0 + i * G;
-        id[i] = t < tokens ? ids[t] : vocab;
-        // the reference kernels leave rows with id >= vocab untouched
-        take[i] = t < tokens && id[i] < vocab;
-    }
-#pragma unroll
-    for (int i = 0; i < TPW; ++i)
-        if (take[i]) stage_row<1, 5, 8>(rows + i * slot, table + static_cast<size_t>(id[i]) * row_bytes, row_bytes,
-                                        lane, kWave);
+    // No early exit before the row is staged, so every kernel argument is
+    // loaded at once and the row loads follow the id directly.  A wavefront
+    // past the last token (tokens >= 1) re-reads the last id; an id >= vocab
+    // stages row 0 -- or nothing, through an empty range, when the table has
+    // no rows -- and both skip their stores (the reference kernels leave
+    // rows with such ids untouched).
+    const uint32_t id = ids[min(t, tokens - 1u)];
+    const bool valid = t < tokens && id < vocab;
+    const auto rs = span_rsrc(table + static_cast<size_t>(valid ? id : 0u) * row_bytes, vocab ? row_bytes : 0u);
+    uint8_t* slot = lds_rows + static_cast<size_t>(wave) * quant_slot_bytes(FMT, hidden);
+    // UNIT: the widest access the table's alignment and row stride allow
+    // (chosen on the host).  Loads per lane per pass: a C4 Q4_0 row is 54
+    // units of 16 bytes, a Q8_0 row 102 units of 16 bytes, a Q6_K row 315
+    // units of 4 bytes.
+    constexpr int kLoads = UNIT == 16 ? (FMT == kQuantQ8_0 ? 2 : 1) : (UNIT == 4 ? 5 : 8);
+    stage_units_wave<kLoads, UNIT>(slot, rs, row_bytes / UNIT, lane);
+    if (!valid) return;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -201,22 +241,18 @@ __global__ __launch_bounds__(64 * WPG) void embed_quant_kernel(const uint8_t* __
     // pass's byte position in the row advances (Q6_K at C4: 6.17-6.24 us
     // against 6.24-6.33 with every offset derived from the column).
     constexpr uint32_t kPassBytes = FMT == kQuantQ6K ? 210u : (FMT == kQuantQ8_0 ? 8u * 34u : 8u * 18u);
-#pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-        if (!take[i]) continue;
-        float* dst = out + static_cast<size_t>(w0 + i * G) * hidden;
-        const uint8_t* pass = rows + i * slot;
-        for (uint32_t c = lane * 4; c < hidden; c += 4 * kWave) {
-            float v[4];
-            if (FMT == kQuantQ6K)
-                q6_k_decode4(pass, lane * 4, v);
-            else if (FMT == kQuantQ8_0)
-                q8_0_decode4(pass, lane * 4, v);
-            else
-                q4_0_decode4(pass, lane * 4, v);
-            stg_nt(dst + c, f32x4{v[0] * scale, v[1] * scale, v[2] * scale, v[3] * scale});
-            pass += kPassBytes;
-        }
+    const auto ro = span_rsrc(out + static_cast<size_t>(t) * hidden, hidden * 4u);
+    const uint8_t* pass = slot;
+    for (uint32_t c = lane * 4; c < hidden; c += 4 * kWave) {
+        float v[4];
+        if (FMT == kQuantQ6K)
+            q6_k_decode4(pass, lane * 4, v);
+        else if (FMT == kQuantQ8_0)
+            q8_0_decode4(pass, lane * 4, v);
+        else
+            q4_0_decode4(pass, lane * 4, v);
+        st_span4<kPolicyWriteThrough>(ro, 4u * c, f32x4{v[0] * scale, v[1] * scale, v[2] * scale, v[3] * scale});
+        pass += kPassBytes;
     }
 }
 
@@ -259,6 +295,7 @@ __global__ __launch_bounds__(256) void ple_seg_kernel(const uint8_t* __restrict_
         stage_row<1, 4, 8>(seg, table + static_cast<size_t>(id) * row_bytes + seg_off, seg_bytes, threadIdx.x,
                            blockDim.x);
     __syncthreads();
+    const auto ro = span_rsrc(out + base, row_elems * 4u);
 #pragma unroll
     for (int f = 0; f < F; ++f) {
         const uint32_t c4 = 256u * (F * sg + f) + threadIdx.x;
@@ -268,7 +305,7 @@ __global__ __launch_bounds__(256) void ple_seg_kernel(const uint8_t* __restrict_
                 q6_k_decode4(seg, 4 * c4 - v0, v);
             else
                 q4_0_decode4(seg, 4 * c4 - v0, v);
-            stg_nt(out + base + 4 * c4, f32x4{(v[0] * embedding_scale + q[f].x) * output_scale,
+            st_span4<kPolicyWriteThrough>(ro, 16u * c4, f32x4{(v[0] * embedding_scale + q[f].x) * output_scale,
                                               (v[1] * embedding_scale + q[f].y) * output_scale,
                                               (v[2] * embedding_scale + q[f].z) * output_scale,
                                               (v[3] * embedding_scale + q[f].w) * output_scale});
@@ -310,33 +347,42 @@ hipError_t launch_embed_f32(hipStream_t stream, const float* table, const uint32
     return hipGetLastError();
 }
 
-template <int FMT, int TPW, int WPG>
+template <int FMT, int WPG>
 hipError_t launch_embed_quant_cfg(hipStream_t stream, const uint8_t* table, const uint32_t* ids, float* out,
                                   uint32_t vocab, uint32_t hidden, uint32_t tokens, float scale) {
-    const uint32_t row_bytes = quant_row_bytes(FMT, hidden);
-    const size_t lds = static_cast<size_t>(WPG) * TPW * ((row_bytes + 15) & ~15u);
-    const uint32_t waves = (tokens + TPW - 1) / TPW;
-    hipLaunchKernelGGL((embed_quant_kernel<FMT, TPW, WPG>), dim3((waves + WPG - 1) / WPG), dim3(64 * WPG), lds,
-                       stream, table, ids, out, vocab, hidden, tokens, scale);
+    const size_t lds = static_cast<size_t>(WPG) * quant_slot_bytes(FMT, hidden);
+    const dim3 grid((tokens + WPG - 1) / WPG), block(64 * WPG);
+    const uint32_t al = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(table)) | quant_row_bytes(FMT, hidden);
+    if ((al & 15u) == 0)
+        hipLaunchKernelGGL((embed_quant_kernel<FMT, WPG, 16>), grid, block, lds, stream, table, ids, out, vocab,
+                           hidden, tokens, scale);
+    else if ((al & 3u) == 0)
+        hipLaunchKernelGGL((embed_quant_kernel<FMT, WPG, 4>), grid, block, lds, stream, table, ids, out, vocab,
+                           hidden, tokens, scale);
+    else
+        hipLaunchKernelGGL((embed_quant_kernel<FMT, WPG, 2>), grid, block, lds, stream, table, ids, out, vocab,
+                           hidden, tokens, scale);
     return hipGetLastError();
 }
 
 template <int FMT>
 hipError_t launch_embed_fmt(hipStream_t stream, const uint8_t* table, const uint32_t* ids, float* out,
                             uint32_t vocab, uint32_t hidden, uint32_t tokens, float scale) {
-    // a wavefront per workgroup for decode batches (so 256 tokens spread over
-    // 256 CUs) and when four rows would not fit 64 KiB of LDS (hidden up to
-    // 65536: one Q6_K row is 53760 bytes)
-    const bool four = tokens >= 2048 && 4u * ((quant_row_bytes(FMT, hidden) + 15) & ~15u) <= 65536u;
-    return four ? launch_embed_quant_cfg<FMT, 1, 4>(stream, table, ids, out, vocab, hidden, tokens, scale)
-                : launch_embed_quant_cfg<FMT, 1, 1>(stream, table, ids, out, vocab, hidden, tokens, scale);
+    // Wavefronts per workgroup, measured on MI355X at C4 (4096 tokens, hidden
+    // 1536; write-through stores, host-selected staging unit): Q4_0 5.09 us
+    // with one, 5.12 with two, 5.19 with four, 5.20-5.25 with eight or
+    // sixteen; Q6_K 5.42 us with two, 5.51-5.58 with one, 5.46 with four.
+    // Decode batches take one (256 tokens spread over 256 CUs), and so do
+    // rows whose two slots would not fit 64 KiB of LDS.
+    const bool two = FMT != kQuantQ4_0 && tokens >= 2048 && 2u * quant_slot_bytes(FMT, hidden) <= 65536u;
+    return two ? launch_embed_quant_cfg<FMT, 2>(stream, table, ids, out, vocab, hidden, tokens, scale)
+               : launch_embed_quant_cfg<FMT, 1>(stream, table, ids, out, vocab, hidden, tokens, scale);
 }
 
-// One token per wavefront, four wavefronts per workgroup.  Measured on
-// MI355X at C4 (4096 tokens, hidden 1536): Q4_0 5.59 us and Q6_K 5.96 us,
-// against 5.34-5.64 and 6.06-6.44 us with one wavefront per workgroup; two or
-// four tokens per wavefront were slower (Q4_0 5.7-7.0 us, Q6_K 7.0-9.1 us):
-// a wavefront's second row waits behind its first.
+// One token per wavefront.  Measured and not kept at C4: two or four tokens
+// per wavefront (Q4_0 5.7-7.0 us, Q6_K 7.0-9.1 us: a wavefront's second row
+// waits behind its first), staging a Q6_K row as 16-byte loads of the aligned
+// span around it (6.7 against 5.6 us).
 hipError_t launch_embed_quant(hipStream_t stream, int format, const uint8_t* table, const uint32_t* ids,
                               float* out, uint32_t vocab, uint32_t hidden, uint32_t tokens, float scale) {
     switch (format) {

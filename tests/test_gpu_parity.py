@@ -305,6 +305,34 @@ def test_embed_quant_shapes(rt, ora, fmt, hidden, tokens):
     assert_bits(f"embed {fmt}", cases.embed_q_gpu(rt, inp, m), cases.embed_q_oracle(ora, inp, m))
 
 
+@pytest.mark.parametrize("fmt", ["q4_0", "q6_k", "q8_0"])
+def test_embed_quant_table_at_any_offset(rt, ora, fmt):
+    """The gather stages a row through the 16-byte-aligned span around it:
+    tables starting at every even skew of a 16-byte line (rows then start
+    at skews 0-14), and at odd addresses, which take the generic staging,
+    give the same bits.  Row widths 1536 (C4) and 8960 (the PLE row); ids
+    include the first and last row."""
+    vocab, tokens = 97, 70
+    for hidden in (1536, 8960):
+        inp, m = cases.embed_q_case(vocab, hidden, tokens, 660 + hidden, fmt == "q6_k", fmt)
+        inp["ids"][:3] = [0, vocab - 1, 0]
+        exp = cases.embed_q_oracle(ora, inp, m)
+        table = inp["table"]
+        fn = {"q4_0": rt.embed_q4_0, "q6_k": rt.embed_q6_k, "q8_0": rt.embed_q8_0}[fmt]
+        ids = rt.upload(inp["ids"])
+        n = tokens * hidden
+        o = rt.empty(n)
+        for off in (0, 2, 4, 6, 10, 14, 1, 7):
+            say(f"embed {fmt} hidden={hidden} table offset {off}")
+            buf = rt.alloc(table.nbytes + 16, np.uint8)
+            t = buf.offset(off, np.uint8).upload(table)
+            rt.memset(o, 0, n * 4)
+            fn(t, ids, o, vocab, hidden, tokens, m["scale"])
+            rt.sync()
+            assert_bits(f"embed {fmt} offset {off}", [o.download(n)], exp)
+            rt.free(buf)
+
+
 def test_embed_q8_0_out_of_range_and_scale(rt, ora):
     """Q8_0 ids at and past the vocabulary leave rows untouched
     (kernels.metal:660); a non-unit scale rounds once after the exact dequant."""
@@ -350,6 +378,12 @@ def test_out_of_range_ids_follow_reference(rt, ora):
         rt.sync()
         exp = (ora.embed_q6_k if q6 else ora.embed_q4_0)(inp["table"], ids, vocab, h, m["scale"], out=sentinel)
         assert_bits("oob untouched", [ob.download(t * h)], [exp])
+        # a table with no rows: every id is out of range and nothing is read or written
+        say(f"empty table q6={q6}")
+        ob = rt.upload(sentinel)
+        (rt.embed_q6_k if q6 else rt.embed_q4_0)(rt.empty(4), ib, ob, 0, h, t, m["scale"])
+        rt.sync()
+        assert_bits("vocab 0 untouched", [ob.download(t * h)], [sentinel])
     table = wl.normal(wl.rng(1), vocab * h)
     tb, ib, ob = rt.upload(table), rt.upload(ids), rt.empty(t * h)
     rt.embed_f32(tb, ib, ob, vocab, h, t)
