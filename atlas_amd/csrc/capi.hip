@@ -907,7 +907,11 @@ int atlas_hip_softcap_argmax_f32_noalloc(atlas_hip_ctx* ctx, const float* logits
          reinterpret_cast<uintptr_t>(selected)) & 3)
         return invalid(ctx, "logits and selected must be 4-byte aligned");
     if (!ctx->argmax_scratch) return invalid(ctx, "the argmax scratch was not resolved for this device");
-    if (atlas::logits_launches(logits, capped, rows, count, atlas::kArgmaxScratchSlots) != 1)
+    // rows that fit one workgroup each never touch the scratch (any row
+    // count, in launches of up to 65535 rows); split rows need all their
+    // partial keys in the scratch at once, in one launch pair
+    if (atlas::logits_row_blocks(logits, capped, rows, count) > 1 &&
+        atlas::logits_launches(logits, capped, rows, count, atlas::kArgmaxScratchSlots) != 1)
         return fail(ctx, ATLAS_ERR_INVALID_INPUT,
                     "invalid buffer/input: rows x workgroups per row exceed the no-allocation argmax scratch "
                     "(%u slots; it holds up to 256 rows of 262144 values, 64 rows of 1048576)",

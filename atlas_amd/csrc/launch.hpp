@@ -174,6 +174,9 @@ hipError_t launch_logits_f32(hipStream_t stream, const float* logits, float* cap
 // (0 if a row needs more slots than that).
 uint32_t logits_launches(const float* logits, const float* capped, uint32_t rows, uint32_t count,
                          uint32_t slot_count);
+// Workgroups per row of launch_logits_f32 for these operands: with one, the
+// argmax is written directly and the workspace is not used.
+uint32_t logits_row_blocks(const float* logits, const float* capped, uint32_t rows, uint32_t count);
 // The library's static scratch for the no-allocation soft cap + argmax:
 // kArgmaxScratchSlots slots (128 KiB per GPU).  argmax_scratch_address gives
 // the current device's copy (hipGetSymbolAddress).

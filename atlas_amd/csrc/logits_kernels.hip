@@ -272,6 +272,10 @@ uint32_t logits_launches(const float* logits, const float* capped, uint32_t rows
     return per == 0 ? 0u : (rows + per - 1) / per;
 }
 
+uint32_t logits_row_blocks(const float* logits, const float* capped, uint32_t rows, uint32_t count) {
+    return row_split(logits, capped, rows, count).blocks;
+}
+
 // ---------------------------------------------------------------------------
 // Scratch of the no-allocation soft cap + argmax entry point: a file-scope
 // device array, one per GPU for the life of the process.  Host code never

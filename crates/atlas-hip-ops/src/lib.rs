@@ -98,6 +98,62 @@ pub enum Reduction {
     Auto,
 }
 
+mod sealed {
+    pub trait Sealed {}
+    impl Sealed for f32 {}
+    impl Sealed for u32 {}
+    impl Sealed for u16 {}
+    impl Sealed for u8 {}
+}
+
+/// Element types a [`DeviceBuffer`] may hold: plain data with no padding and
+/// no invalid bit patterns, so bytes read back from the device are always a
+/// valid value.  Sealed; implemented for `f32`, `u32`, `u16` (binary16 bits)
+/// and `u8` (packed GGUF blocks).
+pub trait DevicePod: Copy + sealed::Sealed {}
+impl DevicePod for f32 {}
+impl DevicePod for u32 {}
+impl DevicePod for u16 {}
+impl DevicePod for u8 {}
+
+fn invalid(msg: String) -> HipError {
+    HipError::InvalidInput(msg)
+}
+
+/// The product of `factors` as an element count; InvalidInput when it
+/// overflows.
+fn extent(factors: &[u64]) -> Result<usize, HipError> {
+    let mut p: u64 = 1;
+    for &f in factors {
+        p = p.checked_mul(f).ok_or_else(|| invalid("buffer extent overflows".into()))?;
+    }
+    usize::try_from(p).map_err(|_| invalid("buffer extent overflows".into()))
+}
+
+/// InvalidInput unless `buf` holds at least `count` elements: the safe
+/// resident ops check every buffer against the elements the kernel touches
+/// before the call, so no argument can make a kernel read or write past a
+/// buffer.
+fn holds<T: DevicePod>(buf: &DeviceBuffer<T>, count: usize, what: &str) -> Result<(), HipError> {
+    if buf.len() < count {
+        return Err(invalid(format!("{what} holds {} elements, the op touches {count}", buf.len())));
+    }
+    Ok(())
+}
+
+/// Bytes of one packed row of `hidden` values (the GGUF block sizes,
+/// crates/atlas-core/src/gguf.rs:16-77); None for a format the gathers do
+/// not take.  The library rejects widths that are not whole blocks.
+fn packed_row_bytes(format: u32, hidden: u32) -> Option<u64> {
+    let h = hidden as u64;
+    match format {
+        ffi::ATLAS_GGUF_Q4_0 => Some(h / 32 * 18),
+        ffi::ATLAS_GGUF_Q8_0 => Some(h / 32 * 34),
+        ffi::ATLAS_GGUF_Q6_K => Some(h / 256 * 210),
+        _ => None,
+    }
+}
+
 /// One HIP device context: `MetalRuntime::new` (crates/atlas-metal/src/lib.rs:909-1061).
 /// Use it from one thread at a time (calls are not re-entrant).
 pub struct HipRuntime {
@@ -170,7 +226,7 @@ impl HipRuntime {
     }
 
     /// A device buffer of `len` elements (uninitialised).
-    pub fn buffer<T: Copy>(&self, len: usize) -> Result<DeviceBuffer<'_, T>, HipError> {
+    pub fn buffer<T: DevicePod>(&self, len: usize) -> Result<DeviceBuffer<'_, T>, HipError> {
         let mut ptr = std::ptr::null_mut();
         let bytes = len.max(1) * std::mem::size_of::<T>();
         self.check(unsafe { ffi::atlas_hip_malloc(self.ctx, bytes, &mut ptr) })?;
@@ -178,7 +234,7 @@ impl HipRuntime {
     }
 
     /// `buffer_from_slice` (crates/atlas-metal/src/lib.rs:1975-2054).
-    pub fn upload<T: Copy>(&self, data: &[T]) -> Result<DeviceBuffer<'_, T>, HipError> {
+    pub fn upload<T: DevicePod>(&self, data: &[T]) -> Result<DeviceBuffer<'_, T>, HipError> {
         let b = self.buffer::<T>(data.len())?;
         let bytes = std::mem::size_of_val(data);
         self.check(unsafe { ffi::atlas_hip_upload(self.ctx, b.ptr, data.as_ptr() as *const c_void, bytes) })?;
@@ -186,10 +242,17 @@ impl HipRuntime {
     }
 
     // -- resident fused ops: one per reference dispatch -----------------------
+    // Each checks its buffers' lengths against the elements the kernel
+    // touches (InvalidInput otherwise) before the call; the library checks
+    // the shapes themselves.
 
     /// `rms_norm_f32` / `rms_norm_decode_batch_f32` (kernels.metal:106-133).
     pub fn rms_norm(&self, x: &DeviceBuffer<f32>, w: &DeviceBuffer<f32>, y: &DeviceBuffer<f32>, rows: u32,
                     hidden: u32, eps: f32) -> Result<(), HipError> {
+        let n = extent(&[rows as u64, hidden as u64])?;
+        holds(x, n, "x")?;
+        holds(y, n, "y")?;
+        holds(w, hidden as usize, "weight")?;
         self.check(unsafe { ffi::atlas_hip_rms_norm_f32(self.ctx, x.ptr(), w.ptr(), y.ptr_mut(), rows, hidden, eps) })
     }
 
@@ -200,6 +263,14 @@ impl HipRuntime {
     pub fn rms_norm_residual(&self, x: &DeviceBuffer<f32>, w: &DeviceBuffer<f32>, residual: &DeviceBuffer<f32>,
                              normalized: Option<&DeviceBuffer<f32>>, out: &DeviceBuffer<f32>, rows: u32,
                              hidden: u32, eps: f32) -> Result<(), HipError> {
+        let count = extent(&[rows as u64, hidden as u64])?;
+        holds(x, count, "x")?;
+        holds(residual, count, "residual")?;
+        holds(out, count, "out")?;
+        holds(w, hidden as usize, "weight")?;
+        if let Some(b) = normalized {
+            holds(b, count, "normalized")?;
+        }
         let n = normalized.map_or(std::ptr::null_mut(), |b| b.ptr_mut());
         self.check(unsafe {
             ffi::atlas_hip_rms_norm_residual_f32(self.ctx, x.ptr(), w.ptr(), residual.ptr(), n, out.ptr_mut(), rows,
@@ -212,6 +283,12 @@ impl HipRuntime {
     pub fn add_rms_norm(&self, x: &DeviceBuffer<f32>, residual: &DeviceBuffer<f32>, w: &DeviceBuffer<f32>,
                         residual_out: &DeviceBuffer<f32>, y: &DeviceBuffer<f32>, rows: u32, hidden: u32,
                         eps: f32) -> Result<(), HipError> {
+        let n = extent(&[rows as u64, hidden as u64])?;
+        holds(x, n, "x")?;
+        holds(residual, n, "residual")?;
+        holds(residual_out, n, "residual_out")?;
+        holds(y, n, "y")?;
+        holds(w, hidden as usize, "weight")?;
         self.check(unsafe {
             ffi::atlas_hip_add_rms_norm_f32(self.ctx, x.ptr(), residual.ptr(), w.ptr(), residual_out.ptr_mut(),
                                             y.ptr_mut(), rows, hidden, eps)
@@ -222,6 +299,11 @@ impl HipRuntime {
     /// (state + norm(x) * w) * scale[0].
     pub fn rms_norm_add_scale(&self, x: &DeviceBuffer<f32>, w: &DeviceBuffer<f32>, state: &DeviceBuffer<f32>,
                               scale: &DeviceBuffer<f32>, rows: u32, hidden: u32, eps: f32) -> Result<(), HipError> {
+        let n = extent(&[rows as u64, hidden as u64])?;
+        holds(x, n, "x")?;
+        holds(state, n, "state")?;
+        holds(w, hidden as usize, "weight")?;
+        holds(scale, 1, "scale")?;
         self.check(unsafe {
             ffi::atlas_hip_rms_norm_add_scale_f32(self.ctx, x.ptr(), w.ptr(), state.ptr_mut(), scale.ptr(), rows,
                                                   hidden, eps)
@@ -234,6 +316,23 @@ impl HipRuntime {
                         k_weight: &DeviceBuffer<f32>, cos: &DeviceBuffer<f32>, sin: &DeviceBuffer<f32>,
                         q_out: &DeviceBuffer<f32>, k_out: &DeviceBuffer<f32>, tokens: u32, q_heads: u32,
                         has_key: bool, head_dim: u32, rope_stride: u32, eps: f32) -> Result<(), HipError> {
+        let qn = extent(&[tokens as u64, q_heads as u64, head_dim as u64])?;
+        holds(q, qn, "q")?;
+        holds(q_out, qn, "q_out")?;
+        holds(q_weight, head_dim as usize, "q_weight")?;
+        if has_key {
+            let kn = extent(&[tokens as u64, head_dim as u64])?;
+            holds(k, kn, "k")?;
+            holds(k_out, kn, "k_out")?;
+            holds(k_weight, head_dim as usize, "k_weight")?;
+        }
+        if tokens > 0 {
+            // row t of the tables is read at t * rope_stride, head_dim / 2 pairs
+            let rows = extent(&[tokens as u64 - 1, rope_stride as u64])?;
+            let tn = rows.checked_add(head_dim as usize / 2).ok_or_else(|| invalid("buffer extent overflows".into()))?;
+            holds(cos, tn, "cos")?;
+            holds(sin, tn, "sin")?;
+        }
         self.check(unsafe {
             ffi::atlas_hip_qk_norm_rope_f32(self.ctx, q.ptr(), k.ptr(), q_weight.ptr(), k_weight.ptr(), cos.ptr(),
                                             sin.ptr(), q_out.ptr_mut(), k_out.ptr_mut(), tokens, q_heads,
@@ -244,12 +343,20 @@ impl HipRuntime {
     /// `silu_f32` + `vector_multiply_f32` (kernels.metal:27-36, 64-69).
     pub fn swiglu(&self, gate: &DeviceBuffer<f32>, up: &DeviceBuffer<f32>, out: &DeviceBuffer<f32>, n: u64)
                   -> Result<(), HipError> {
+        let count = extent(&[n])?;
+        holds(gate, count, "gate")?;
+        holds(up, count, "up")?;
+        holds(out, count, "out")?;
         self.check(unsafe { ffi::atlas_hip_swiglu_f32(self.ctx, gate.ptr(), up.ptr(), out.ptr_mut(), n) })
     }
 
     /// `gelu_multiply_f32` (kernels.metal:773-784).
     pub fn geglu(&self, gate: &DeviceBuffer<f32>, up: &DeviceBuffer<f32>, out: &DeviceBuffer<f32>, n: u64)
                  -> Result<(), HipError> {
+        let count = extent(&[n])?;
+        holds(gate, count, "gate")?;
+        holds(up, count, "up")?;
+        holds(out, count, "out")?;
         self.check(unsafe { ffi::atlas_hip_geglu_f32(self.ctx, gate.ptr(), up.ptr(), out.ptr_mut(), n) })
     }
 
@@ -257,6 +364,9 @@ impl HipRuntime {
     #[allow(clippy::too_many_arguments)]
     pub fn embed_f32(&self, table: &DeviceBuffer<f32>, ids: &DeviceBuffer<u32>, out: &DeviceBuffer<f32>, vocab: u32,
                      hidden: u32, tokens: u32, scale: f32) -> Result<(), HipError> {
+        holds(table, extent(&[vocab as u64, hidden as u64])?, "table")?;
+        holds(ids, tokens as usize, "ids")?;
+        holds(out, extent(&[tokens as u64, hidden as u64])?, "out")?;
         self.check(unsafe {
             ffi::atlas_hip_embed_f32(self.ctx, table.ptr(), ids.ptr(), out.ptr_mut(), vocab, hidden, tokens, scale)
         })
@@ -274,6 +384,10 @@ impl HipRuntime {
             ffi::ATLAS_GGUF_Q6_K => ffi::atlas_hip_embed_q6_k,
             other => return Err(HipError::InvalidInput(format!("unsupported packed embedding format {other}"))),
         };
+        let row = packed_row_bytes(format, hidden).unwrap_or(0);
+        holds(table, extent(&[vocab as u64, row])?, "table")?;
+        holds(ids, tokens as usize, "ids")?;
+        holds(out, extent(&[tokens as u64, hidden as u64])?, "out")?;
         self.check(unsafe { f(self.ctx, table.ptr(), ids.ptr(), out.ptr_mut(), vocab, hidden, tokens, scale) })
     }
 
@@ -283,6 +397,14 @@ impl HipRuntime {
                out: &DeviceBuffer<f32>, vocab: u32, layers: u32, width: u32, tokens: u32, embedding_scale: f32,
                output_scale: f32) -> Result<(), HipError> {
         let f = if q6_k { ffi::atlas_hip_ple_q6_k } else { ffi::atlas_hip_ple_q4_0 };
+        let values = extent(&[layers as u64, width as u64])?;
+        let fmt = if q6_k { ffi::ATLAS_GGUF_Q6_K } else { ffi::ATLAS_GGUF_Q4_0 };
+        let row = u32::try_from(values).ok().and_then(|v| packed_row_bytes(fmt, v)).unwrap_or(0);
+        holds(table, extent(&[vocab as u64, row])?, "table")?;
+        holds(ids, tokens as usize, "ids")?;
+        let n = extent(&[tokens as u64, values as u64])?;
+        holds(projection, n, "projection")?;
+        holds(out, n, "out")?;
         self.check(unsafe {
             f(self.ctx, table.ptr(), ids.ptr(), projection.ptr(), out.ptr_mut(), vocab, layers, width, tokens,
               embedding_scale, output_scale)
@@ -297,14 +419,14 @@ impl Drop for HipRuntime {
 }
 
 /// A device allocation of `len` elements of `T`, freed on drop: `GpuBuffer`.
-pub struct DeviceBuffer<'rt, T: Copy> {
+pub struct DeviceBuffer<'rt, T: DevicePod> {
     rt: &'rt HipRuntime,
     ptr: *mut c_void,
     len: usize,
     _t: PhantomData<T>,
 }
 
-impl<T: Copy> DeviceBuffer<'_, T> {
+impl<T: DevicePod> DeviceBuffer<'_, T> {
     pub fn len(&self) -> usize {
         self.len
     }
@@ -328,7 +450,7 @@ impl<T: Copy> DeviceBuffer<'_, T> {
     }
 }
 
-impl<T: Copy> Drop for DeviceBuffer<'_, T> {
+impl<T: DevicePod> Drop for DeviceBuffer<'_, T> {
     fn drop(&mut self) {
         unsafe {
             ffi::atlas_hip_free(self.rt.ctx, self.ptr);

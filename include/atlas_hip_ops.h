@@ -416,11 +416,15 @@ int atlas_hip_softcap_argmax_f32(atlas_hip_ctx *ctx, const float *logits, float 
  * harnesses that forbid hipMalloc).  Same arguments, validation and results;
  * the per-workgroup partial keys go to a 128 KiB static device array of the
  * library (16384 slots, one copy per GPU, resolved by atlas_hip_init)
- * instead of the context's workspace, and the call allocates nothing and
- * makes one launch pair.  Sizes whose rows x workgroups per row exceed the
- * 16384 slots are rejected with ATLAS_ERR_INVALID_INPUT (256 rows of 262144
- * values fit, as do 64 rows of 1048576).  Every call on one GPU shares the
- * array: calls that overlap on one GPU (two streams or contexts) race. */
+ * instead of the context's workspace, and the call allocates nothing.  A
+ * row longer than one workgroup's share (1024 values; 4096 in batches of
+ * 2^22 values or more) is split over several workgroups whose partial keys
+ * must all fit the 16384 slots in one launch pair: sizes whose rows x
+ * workgroups per row exceed them are rejected with ATLAS_ERR_INVALID_INPUT
+ * (256 rows of 262144 values fit, as do 64 rows of 1048576).  Rows of one
+ * workgroup use no slots, at any row count (launches of up to 65535 rows).
+ * Every call on one GPU shares the array: calls that overlap on one GPU (two
+ * streams or contexts) race. */
 int atlas_hip_softcap_argmax_f32_noalloc(atlas_hip_ctx *ctx, const float *logits, float *capped,
                                          uint32_t *selected, uint32_t rows, uint32_t count, float cap);
 

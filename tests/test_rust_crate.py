@@ -81,3 +81,25 @@ def test_safe_layer_calls_declared_functions_and_mirrors_neural_ops():
     build = open(os.path.join(CRATE, "build.rs")).read()
     assert "rustc-link-lib=dylib=atlas_hip_ops" in build
     assert 'links = "atlas_hip_ops"' in open(os.path.join(CRATE, "Cargo.toml")).read()
+
+
+def test_safe_resident_ops_check_buffer_lengths():
+    """Every safe method of HipRuntime that enqueues a kernel checks each
+    buffer it passes against the elements the op touches (`holds`) before
+    the FFI call, and device buffers hold only the sealed plain-data types
+    (no `T: Copy` bound that would admit bool, enums or padded structs)."""
+    lib = open(os.path.join(CRATE, "src", "lib.rs")).read()
+    impl = lib[lib.index("impl HipRuntime {"):lib.index("impl Drop for HipRuntime")]
+    ops = re.split(r"\n    pub fn ", impl)[1:]
+    enqueuing = [m for m in ops if re.search(r"ffi::atlas_hip_(rms|add_rms|qk|swiglu|geglu|embed|ple)", m)
+                 or "atlas_hip_embed_q" in m or "atlas_hip_ple_q" in m]
+    assert len(enqueuing) >= 9, len(enqueuing)
+    for body in enqueuing:
+        name = body.split("(", 1)[0]
+        call = body.index("self.check(")
+        assert "holds(" in body[:call], f"{name} calls the library before checking its buffers"
+        params = re.findall(r"(\w+): (?:Option<)?&DeviceBuffer", body.split(") ->", 1)[0])
+        for p in params:
+            assert re.search(rf"holds\({p}\b|Some\(b\) = {p}", body[:call]), (name, p)
+    assert "T: Copy" not in lib
+    assert re.search(r"pub trait DevicePod: Copy \+ sealed::Sealed \{\}", lib)
