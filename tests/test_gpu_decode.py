@@ -91,6 +91,31 @@ def test_decode_step_eager_and_graph_replays(rt, ora, batch, vocab):
         step.close()
 
 
+def test_decode_step_under_auto_reduction(rt_auto, ora):
+    """The library's default reduction, which bench.py --decode and every
+    integrator use: every norm of the C5 chain is an epilogue that can cancel
+    (residual, add-scale) or the QK-norm, so AUTO keeps the sequential fold and
+    the chain is bit-identical to the oracle, eager and replayed."""
+    shape = wl.DecodeShape(batch=64)
+    say(f"building decode step {shape} vocab=8192 (AUTO)")
+    step = GemmaDecodeStep(rt_auto, shape, seed=4, vocab=8192)
+    try:
+        exp = oracle_step(ora, step)
+        say("eager step (AUTO)")
+        step.enqueue()
+        rt_auto.sync()
+        assert_same(step.results(), exp, "eager AUTO")
+        step.capture()
+        for i in range(2):
+            rt_auto.memset(step.out["state"], 0, shape.batch * shape.hidden * 4)
+            say(f"replay {i} (AUTO)")
+            step.replay()
+            rt_auto.sync()
+            assert_same(step.results(), exp, f"replay {i} AUTO")
+    finally:
+        step.close()
+
+
 def test_graph_capture_rejects_synchronising_calls(rt):
     from atlas_amd import OperatorError
     rt.graph_begin()
