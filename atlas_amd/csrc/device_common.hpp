@@ -97,12 +97,14 @@ __device__ __forceinline__ float exp_reduced(float x, int& n) {
     return p;
 }
 
-// e^x for |x| < 87 (n in [-126, 127]): one exact scale by 2^n.  Outside that
-// domain the value is meaningless and must be selected away by the caller.
+// e^x for |x| < 87 (n in [-125, 126], so p * 2^n is a normal number and the
+// scale is exact: ldexp gives the product p * 2^n bit for bit, in one
+// instruction instead of building 2^n and multiplying).  Outside that domain
+// the value is meaningless and must be selected away by the caller.
 __device__ __forceinline__ float exp_small_f32(float x) {
     int n;
     const float p = exp_reduced(x, n);
-    return p * __uint_as_float(static_cast<uint32_t>(n + 127) << 23);
+    return __builtin_ldexpf(p, n);
 }
 
 // e^x over the whole binary32 range.  Outside n in [-126, 127] the scale is
@@ -275,6 +277,26 @@ __device__ __forceinline__ float materialize(float v) {
 
 __device__ __forceinline__ uint16_t f2h(float v) {  // IEEE RNE of the f32 value
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(materialize(v)));
+}
+
+// a * h with one rounding, where h is the low (HI = 0) or high (HI = 1)
+// binary16 half of `pair`: v_fma_mix_f32 widens the half exactly inside the
+// multiply and adds -0.0f (held in a register), which changes no product (a
+// zero product keeps its sign) -- the bits of a * h2f(half), one VALU
+// instruction instead of a conversion and a multiply.  (Written out because
+// the compiler folds fma(a, b, -0) back into a multiply of the converted
+// operand.)
+template <int HI>
+__device__ __forceinline__ float mul_f16_half(float a, uint32_t pair) {
+    float r;
+    const float neg_zero = -0.0f;
+    if constexpr (HI)
+        __asm__("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]"
+                : "=v"(r) : "v"(a), "v"(pair), "s"(neg_zero));
+    else
+        __asm__("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[0,1,0]"
+                : "=v"(r) : "v"(a), "v"(pair), "s"(neg_zero));
+    return r;
 }
 
 // Sequential f32 fold of n4 (<= 64) float4 of squares from LDS into s, in

@@ -701,21 +701,43 @@ __global__ __launch_bounds__(256) void rope_half_f16_kernel(const uint16_t* x0, 
 // (NI head steps per lane, clamped to a valid head and never stored past the
 // end).  Same roundings as rope_half_f*_unit: (x0*c) - (x1*s) for the first
 // half, (x0*s) + (x1*c) for the second.
-template <bool F16, int NI>
+//
+// GSH = log2(G) when it is 2 or 3 (G = 4: f16 head_dim 64; G = 8: f32
+// head_dim 64, f16 head_dim 128): the lanes of the second half hold their
+// vectors in reverse order (lane G + j holds vector 2G - 1 - j), so a lane's
+// partner is its mirror within the 2G-lane group and the exchange is one
+// DPP move per dword (row_half_mirror / row_mirror) instead of a cross-lane
+// shuffle through the LDS crossbar.  GSH = -1: G from g_shift at run time,
+// natural order, shuffle exchange.
+template <int GSH>
+__device__ __forceinline__ uint32_t rope_partner(uint32_t own, uint32_t G) {
+    if constexpr (GSH == 2)
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(own), 0x141, 0xf, 0xf, false));
+    else if constexpr (GSH == 3)
+        return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(own), 0x140, 0xf, 0xf, false));
+    else
+        return static_cast<uint32_t>(__shfl_xor(static_cast<int>(own), static_cast<int>(G), kWave));
+}
+
+template <bool F16, int NI, int GSH>
 __global__ __launch_bounds__(256) void rope_half_token_kernel(const uint8_t* x0, uint8_t* out0, uint32_t heads0,
                                                               const uint8_t* x1, uint8_t* out1, uint32_t heads1,
                                                               const float* cosine, const float* sine,
                                                               uint32_t tokens, uint32_t head_dim,
-                                                              uint32_t rope_stride, uint32_t g_shift) {
+                                                              uint32_t rope_stride, uint32_t g_shift_rt) {
     constexpr uint32_t V = F16 ? 8 : 4;
     constexpr uint32_t kEsz = F16 ? 2 : 4;
+    constexpr bool kMirror = GSH >= 0;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= tokens) return;
+    const uint32_t g_shift = kMirror ? static_cast<uint32_t>(GSH) : g_shift_rt;
     const uint32_t G = 1u << g_shift;
     const uint32_t c = lane & (2 * G - 1), hl = lane >> (g_shift + 1);
     const bool first = c < G;
-    const uint32_t g = c & (G - 1);
+    // the vector of the head row this lane holds, and its pair group
+    const uint32_t vec = first || !kMirror ? c : 3 * G - 1 - c;
+    const uint32_t g = vec & (G - 1);
     const uint32_t hps = 32u >> g_shift;  // heads per step
     const uint32_t heads = heads0 + heads1;
     const size_t row_bytes = static_cast<size_t>(head_dim) * kEsz;
@@ -724,7 +746,7 @@ __global__ __launch_bounds__(256) void rope_half_token_kernel(const uint8_t* x0,
     ld_tab<V>(sine + static_cast<size_t>(t) * rope_stride + g * V, sn);
     auto head_offset = [&](uint32_t h, bool second) -> size_t {
         return (second ? static_cast<size_t>(t) * heads1 + (h - heads0) : static_cast<size_t>(t) * heads0 + h) *
-                   row_bytes + c * 16u;
+                   row_bytes + vec * 16u;
     };
     u32x4r v[NI];
 #pragma unroll
@@ -739,7 +761,7 @@ __global__ __launch_bounds__(256) void rope_half_token_kernel(const uint8_t* x0,
         const uint32_t own[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
         uint32_t par[4];
 #pragma unroll
-        for (int w = 0; w < 4; ++w) par[w] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(own[w]), static_cast<int>(G), kWave));
+        for (int w = 0; w < 4; ++w) par[w] = rope_partner<GSH>(own[w], G);
         const uint32_t h = hl + static_cast<uint32_t>(i) * hps;
         if (h < heads) {
             const bool second = h >= heads0;
@@ -749,11 +771,13 @@ __global__ __launch_bounds__(256) void rope_half_token_kernel(const uint8_t* x0,
             for (int w = 0; w < 4; ++w) {
                 const uint32_t wa = first ? own[w] : par[w], wb = first ? par[w] : own[w];
                 if constexpr (F16) {
-                    const float xa0 = h2f(static_cast<uint16_t>(wa)), xa1 = h2f(static_cast<uint16_t>(wa >> 16));
-                    const float xb0 = h2f(static_cast<uint16_t>(wb)), xb1 = h2f(static_cast<uint16_t>(wb >> 16));
+                    // each product rounded once (the f16 operand widens inside
+                    // the multiply), then the sum or difference
                     const float c0 = cs[2 * w], c1 = cs[2 * w + 1], s0 = sn[2 * w], s1 = sn[2 * w + 1];
-                    const float y0 = first ? xa0 * c0 - xb0 * s0 : xa0 * s0 + xb0 * c0;
-                    const float y1 = first ? xa1 * c1 - xb1 * s1 : xa1 * s1 + xb1 * c1;
+                    const float pa0 = mul_f16_half<0>(first ? c0 : s0, wa), pb0 = mul_f16_half<0>(first ? s0 : c0, wb);
+                    const float pa1 = mul_f16_half<1>(first ? c1 : s1, wa), pb1 = mul_f16_half<1>(first ? s1 : c1, wb);
+                    const float y0 = first ? pa0 - pb0 : pa0 + pb0;
+                    const float y1 = first ? pa1 - pb1 : pa1 + pb1;
                     o[w] = static_cast<uint32_t>(f2h(y0)) | (static_cast<uint32_t>(f2h(y1)) << 16);
                 } else {
                     const float xa = __uint_as_float(wa), xb = __uint_as_float(wb);
@@ -795,10 +819,17 @@ bool launch_rope_half_token(hipStream_t stream, const void* x0, void* out0, uint
     const uint8_t* a1 = static_cast<const uint8_t*>(x1);
     uint8_t* b0 = static_cast<uint8_t*>(out0);
     uint8_t* b1 = static_cast<uint8_t*>(out1);
-#define ATLAS_ROPE_TOKEN_CASE(N)                                                                             \
-    case N:                                                                                                  \
-        hipLaunchKernelGGL((rope_half_token_kernel<F16, N>), grid, dim3(256), 0, stream, a0, b0, heads0, a1, \
-                           b1, heads1, cosine, sine, tokens, head_dim, rope_stride, g_shift);                \
+#define ATLAS_ROPE_TOKEN_CASE(N)                                                                                 \
+    case N:                                                                                                      \
+        if (g_shift == 2)                                                                                        \
+            hipLaunchKernelGGL((rope_half_token_kernel<F16, N, 2>), grid, dim3(256), 0, stream, a0, b0, heads0, a1, \
+                               b1, heads1, cosine, sine, tokens, head_dim, rope_stride, g_shift);                \
+        else if (g_shift == 3)                                                                                   \
+            hipLaunchKernelGGL((rope_half_token_kernel<F16, N, 3>), grid, dim3(256), 0, stream, a0, b0, heads0, a1, \
+                               b1, heads1, cosine, sine, tokens, head_dim, rope_stride, g_shift);                \
+        else                                                                                                     \
+            hipLaunchKernelGGL((rope_half_token_kernel<F16, N, -1>), grid, dim3(256), 0, stream, a0, b0, heads0,  \
+                               a1, b1, heads1, cosine, sine, tokens, head_dim, rope_stride, g_shift);            \
         return true;
     switch (ni) {
         ATLAS_ROPE_TOKEN_CASE(1) ATLAS_ROPE_TOKEN_CASE(2) ATLAS_ROPE_TOKEN_CASE(3) ATLAS_ROPE_TOKEN_CASE(4)

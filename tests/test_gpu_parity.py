@@ -542,3 +542,32 @@ def test_rope_half_qk_one_launch(rt, ora, f16, tokens, q_heads, k_heads, head_di
         rt.sync()
         got_k = ko.download(kraw.size, dt)[k_offset:k_offset + k_inp["x"].size]
         assert_bits(f"rope_half_qk k_offset={k_offset}", [qo.download(q_inp["x"].size, dt), got_k], exp)
+
+
+def test_swiglu_f16_zero_signs_and_specials(rt, ora):
+    """FP16 SwiGLU multiplies the activated gate by `up` with the f16 operand
+    widened inside the multiply: products of +-0 keep their signs, subnormal
+    and extreme `up` values round once, inf and NaN propagate.  The first
+    4096 values hold only gates below 87 in magnitude (the in-range path of
+    every wavefront), the rest mix in infinite, NaN and saturating gates
+    (the guarded path)."""
+    h16 = lambda a: np.asarray(a, np.float16).view(np.uint16)
+    r = wl.rng(4242)
+    n = 8192
+    g = r.standard_normal(n).astype(np.float32) * np.float32(3.0)
+    u = r.standard_normal(n).astype(np.float32)
+    specials_u = np.array([0.0, -0.0, 6e-8, -6e-8, 6.1e-5, 65504.0, -65504.0, 1e-3], np.float32)
+    u[:4096:7] = np.resize(specials_u, u[:4096:7].size)
+    g[:4096:5] = np.resize(np.array([0.0, -0.0, 86.9, -86.9, 6e-8, -1e-4], np.float32), g[:4096:5].size)
+    g[4096::3] = np.resize(np.array([np.inf, -np.inf, np.nan, 100.0, -100.0, 65504.0], np.float32), g[4096::3].size)
+    u[4096::4] = np.resize(np.array([np.inf, -np.inf, np.nan, 0.0, -0.0], np.float32), u[4096::4].size)
+    gb, ub = h16(g), h16(u)
+    say("swiglu f16 zero signs and specials")
+    got = cases.swiglu_f16_gpu(rt, {"gate": gb, "up": ub}, {"n": n})
+    exp = np.asarray(ora.swiglu_f16(gb, ub), np.uint16)
+    g16, e16 = np.asarray(got[0], np.uint16), exp
+    same = (g16 == e16) | (np.isnan(g16.view(np.float16)) & np.isnan(e16.view(np.float16)))
+    assert same.all(), f"{int((~same).sum())} of {n} differ; first at {int(np.nonzero(~same)[0][0])}"
+    # the zero products keep their signs
+    zero = (e16 & 0x7fff) == 0
+    assert zero.sum() > 100 and np.array_equal(g16[zero], e16[zero])
