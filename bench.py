@@ -303,16 +303,76 @@ class ConfigOps(Ops):
 
 
 
-def time_launches(rt, launch, sets, iters, batches=5):
+class _RecordingLib:
+    """Records the C-ABI calls made through it: (entry point, arguments
+    converted to their ctypes types once) instead of making them."""
+
+    def __init__(self, lib, calls):
+        self._lib, self._calls = lib, calls
+
+    def __getattr__(self, name):
+        fn = getattr(self._lib, name)
+
+        def record(*args):
+            conv = tuple(a if isinstance(a, t) else t(a) for t, a in zip(fn.argtypes, args))
+            self._calls.append((fn, conv))
+            return 0
+
+        return record
+
+
+class _Recorder:
+    """Stands in for a HipRuntime while an op's launcher runs once on the
+    host: the runtime's method runs with this object as `self` and every
+    C-ABI call it would make is recorded instead."""
+
+    def __init__(self, rt):
+        self.rt, self.ctx, self.calls = rt, rt.ctx, []
+        self.lib = _RecordingLib(rt.lib, self.calls)
+
+    def _check(self, rc):
+        pass
+
+    def __getattr__(self, name):
+        return getattr(type(self.rt), name).__get__(self)
+
+
+def bind_launch(rt, launch, s):
+    """The op launch `launch(rt, s)` as a list of (C entry point, converted
+    arguments): the timed loops call the library directly, so what they time
+    is the launches themselves and not the Python wrapper around each one
+    (a Rust or C caller has none).  Every call still goes through the same
+    C-ABI entry point with its argument checks."""
+    rec = _Recorder(rt)
+    launch(rec, s)
+    if not rec.calls:
+        raise RuntimeError("the op launcher made no library call to bind")
+    return rec.calls
+
+
+def run_bound(rt, calls):
+    for fn, args in calls:
+        rc = fn(*args)
+        if rc:
+            rt._check(rc)
+
+
+def time_launches(rt, launch, sets, iters, batches=5, bind=True):
     """Milliseconds per launch: the median over `batches` runs of iters /
     batches back-to-back launches (HIP events on the library stream), after
     iters / 2 untimed launches.  An op is timed right after its buffer sets
     were uploaded, with the GPU idle meanwhile; with 50 warm-up launches the
     first 1000 timed ones of the C4 Q6_K gather measured 5.58 us against 5.44
-    for the next 1000."""
+    for the next 1000.  bind: `launch` is a runtime op, timed as its bound
+    C-ABI calls (bind_launch); otherwise it is called as given."""
+    if bind:
+        bound = [bind_launch(rt, launch, st) for st in sets]
+        go = lambda i: run_bound(rt, bound[i % len(bound)])  # noqa: E731
+    else:
+        go = lambda i: launch(rt, sets[i % len(sets)])  # noqa: E731
     warm = max(3, iters // 2)
     for i in range(warm):
-        launch(rt, sets[i % len(sets)])
+        go(i)
     rt.sync()
     n = max(1, iters // batches)
     a, b = rt.event(), rt.event()
@@ -320,7 +380,7 @@ def time_launches(rt, launch, sets, iters, batches=5):
     for _ in range(batches):
         rt.record(a)
         for i in range(n):
-            launch(rt, sets[i % len(sets)])
+            go(i)
         rt.record(b)
         rt.sync()
         per.append(rt.elapsed_ms(a, b) / n)
@@ -386,7 +446,7 @@ class StreamFloor:
                 if rc != 0:
                     raise RuntimeError(f"stream floor launch failed: HIP error {rc}")
 
-            result[kind] = time_launches(rt, launch, list(range(nsets)), iters) * 1e3
+            result[kind] = time_launches(rt, launch, list(range(nsets)), iters, bind=False) * 1e3
         return result
 
     def gather_us(self, sets, table, ids, out, row_bytes, vocab, tokens, out_row_bytes, iters):
@@ -401,7 +461,7 @@ class StreamFloor:
             if rc != 0:
                 raise RuntimeError(f"gather floor launch failed: HIP error {rc}")
 
-        return time_launches(rt, launch, sets, iters) * 1e3
+        return time_launches(rt, launch, sets, iters, bind=False) * 1e3
 
     def calls_us(self, in_bytes, out_bytes, n, distinct, iters, graphs=True):
         """Microseconds per launch of every shape, {kind: us}, when n launches
@@ -922,10 +982,10 @@ def main():
     names = list(ops.table)
     sets = ops.build_sets(rt, names, args.step_sets, arena)
 
+    bound = [[call for nm in names for call in bind_launch(rt, ops.table[nm][3], st)] for st in sets]
+
     def step(i):
-        s = sets[i % len(sets)]
-        for nm in names:
-            ops.table[nm][3](rt, s)
+        run_bound(rt, bound[i % len(bound)])
 
     for i in range(args.warmup):
         step(i)

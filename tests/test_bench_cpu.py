@@ -114,3 +114,47 @@ def test_buffer_sets_carved_from_one_arena():
         pass
     else:
         raise AssertionError("a request beyond the arena must be refused")
+
+
+def test_bound_launches_make_the_same_library_calls():
+    """bench.py times each op through bind_launch: the runtime method runs
+    once against a recorder, and the timed loop replays the recorded C-ABI
+    calls (same entry point, same converted arguments, return codes still
+    checked); a launcher that makes no library call is refused."""
+    import ctypes
+
+    import pytest
+
+    from atlas_amd.runtime import HipRuntime, _ptr
+
+    made = []
+
+    class Entry:
+        argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_float]
+
+        def __call__(self, *args):
+            made.append(args)
+            return 0
+
+    class Lib:
+        atlas_hip_rms_norm_f32 = Entry()
+
+    class FakeRuntime(HipRuntime):
+        def __init__(self):  # no device: only what the recorder reads
+            self.lib, self.ctx = Lib(), ctypes.c_void_p(0x1000)
+
+        def probe(self, x, n, eps):
+            self._check(self.lib.atlas_hip_rms_norm_f32(self.ctx, _ptr(x), n, eps))
+
+    rt = FakeRuntime()
+    calls = bench.bind_launch(rt, lambda r, s: r.probe(s["x"], 7, 1e-6), {"x": 0x2000})
+    assert len(calls) == 1 and made == []          # recorded, not made
+    fn, args = calls[0]
+    assert fn is Lib.atlas_hip_rms_norm_f32
+    assert [type(a) for a in args] == Entry.argtypes
+    assert args[1].value == 0x2000 and args[2].value == 7 and abs(args[3].value - 1e-6) < 1e-12
+    bench.run_bound(rt, calls)
+    bench.run_bound(rt, calls)
+    assert len(made) == 2 and all(a is b for a, b in zip(made[0], made[1]))   # the same converted arguments
+    with pytest.raises(RuntimeError):
+        bench.bind_launch(rt, lambda r, s: None, {})
