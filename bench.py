@@ -617,11 +617,13 @@ def cpu_baseline(wl, budget_s=1.0, max_threads=16, host=None):
     CPU operators) on the same step's ops, timed on this host: each op alone
     over 64-token slices of the full-size inputs (the 262144-row tables
     included, so gathers read cache-cold rows), for `budget_s` seconds on one
-    thread and then `budget_s` on every host core of the box's share (at most
-    max_threads threads, each on its own token slices; ctypes releases the
-    GIL during each C call).  Per op: GB/s (algorithmic bytes) and tokens/s
-    on 1 and N cores; the step's tokens/s is 1 / the sum of the ops' seconds
-    per token.  `host`: the step's full-size inputs (Ops.host); generated
+    thread and then `budget_s` on every host core of the box's share (the
+    affinity set, capped at OMP_NUM_THREADS -- 16 per GPU on the MI355X
+    boxes -- and at max_threads; each thread on its own token slices; ctypes
+    releases the GIL during each C call).  The line records the affinity
+    count, the share and the threads used.  Per op: GB/s (algorithmic bytes)
+    and tokens/s on 1 and N cores; the step's tokens/s is 1 / the sum of the
+    ops' seconds per token.  `host`: the step's full-size inputs (Ops.host); generated
     here when None.  The oracle is test infrastructure; here it is the
     reported CPU baseline, never the product."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -693,7 +695,11 @@ def cpu_baseline(wl, budget_s=1.0, max_threads=16, host=None):
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count() or 1
-    threads = max(1, min(max_threads, cores))
+    # the host CPUs this process may use (affinity) and the share of them the
+    # GPU box grants one GPU's job (OMP_NUM_THREADS, set to 16 there; a pool
+    # sized past the share competes with the driver's own work)
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or max_threads
+    threads = max(1, min(share, cores, max_threads))
     ops, s1, sn = {}, 0.0, 0.0
     for name, (bpt, fn) in per_tok.items():
         one = run(fn, 1)
@@ -702,6 +708,7 @@ def cpu_baseline(wl, budget_s=1.0, max_threads=16, host=None):
         ops[name] = {"GB/s_1core": round(bpt / one / 1e9, 3), f"GB/s_{threads}cores": round(bpt / many / 1e9, 3),
                      "tokens_per_s_1core": round(1.0 / one, 1), f"tokens_per_s_{threads}cores": round(1.0 / many, 1)}
     return {"value": round(1.0 / sn, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "affinity_cores": cores, "cpu_share": share,
             "single_thread": round(1.0 / s1, 1), "ops": ops,
             "sample": f"each op of the step alone over 64-token slices of the full-size inputs (262144-row "
                       f"tables), the C oracle built -O3 -ffp-contract=off: {budget_s:g} s on 1 thread and "

@@ -3,7 +3,7 @@
  *
  * TEST INFRASTRUCTURE ONLY (parity checker and CPU baseline); see the header
  * atlas_oracle.h for the arithmetic contract and the checks that pin each
- * function.  Build: oracle/Makefile (-O2 -ffp-contract=off, no fast-math).
+ * function.  Build: oracle/Makefile (-O3 -ffp-contract=off, no fast-math).
  *
  * Reference citations are `path:line` into bisegni/atlas.
  */
