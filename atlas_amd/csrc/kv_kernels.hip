@@ -415,35 +415,40 @@ __device__ __forceinline__ void store_row(const f32x4 (&x)[V4], uint8_t* dst, ui
     }
 }
 
-// Rows of kv_width 256 for the eight-token kernel (one f32x4 per lane per
+// Rows of kv_width 256 for the many-token kernel (one f32x4 per lane per
 // row).  Explicit global casts keep the stores global, not flat: LDS waits
 // do not count global stores, and they do count flat ones.
 typedef __attribute__((address_space(1))) f32x4 global_f32x4;
 
-// Store two f32 rows, scaled by inv[i] when NORM; a row whose `ok` is false
+// Store N f32 rows, scaled by inv[i] when NORM; a row whose `ok` is false
 // stores nothing.
-template <bool NORM>
-__device__ __forceinline__ void store_f32_rows2(const f32x4 (&x)[2], const float (&inv)[2], uint8_t* const (&dst)[2],
-                                                const bool (&ok)[2], uint32_t lane) {
+template <int N, bool NORM>
+__device__ __forceinline__ void store_f32_rows(const f32x4 (&x)[N], const float (&inv)[N], uint8_t* const (&dst)[N],
+                                               const bool (&ok)[N], uint32_t lane) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < N; ++i) {
         const f32x4 y = NORM ? f32x4{x[i].x * inv[i], x[i].y * inv[i], x[i].z * inv[i], x[i].w * inv[i]} : x[i];
         if (ok[i]) __builtin_nontemporal_store(y, (global_f32x4*)dst[i] + lane);
     }
 }
 
-// Encode two rows (scaled by inv[i] when NORM; bmax: their block_max before
+// Encode N rows (scaled by inv[i] when NORM; bmax: their block_max before
 // scaling) side by side into the LDS row buffers at `lds`.
-template <int FMT, bool NORM>
-__device__ __forceinline__ void encode_rows2(const f32x4 (&x)[2], const float (&inv)[2], const float (&bmax)[2],
-                                             uint8_t* lds, uint32_t lane) {
+template <int FMT, int N, bool NORM>
+__device__ __forceinline__ void encode_rows(const f32x4 (&x)[N], const float (&inv)[N], const float (&bmax)[N],
+                                            uint8_t* lds, uint32_t lane) {
     constexpr uint32_t kRowBytes = 8u * (FMT == kKvQ8_0 ? 34u : 18u);
-    uint8_t* const rows[2] = {lds, lds + kRowBytes};
-    const uint32_t blk[2] = {lane / 8u, lane / 8u};
-    encode_items<FMT, 2, NORM>(x, inv, bmax, rows, blk, lane & 7u);
+    uint8_t* rows[N];
+    uint32_t blk[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        rows[i] = lds + i * kRowBytes;
+        blk[i] = lane / 8u;
+    }
+    encode_items<FMT, N, NORM>(x, inv, bmax, rows, blk, lane & 7u);
 }
 
-// Two encoded rows side by side in LDS at `lds` (2 x 17 / 2 x 9 16-byte
+// N encoded rows side by side in LDS at `lds` (N x 17 / N x 9 16-byte
 // chunks, one per lane): store them (a row whose `ok` is false stores
 // nothing) and return the store's address and data.  The hardware reads a
 // vector store's registers after issue, so the compiler makes the first
@@ -455,15 +460,23 @@ struct PendingStore {
     f32x4 data;
 };
 
-template <int FMT>
-__device__ __forceinline__ PendingStore flush_rows2(const uint8_t* lds, uint8_t* const (&dst)[2], const bool (&ok)[2],
-                                                    uint32_t lane) {
+template <int FMT, int N>
+__device__ __forceinline__ PendingStore flush_rows(const uint8_t* lds, uint8_t* const (&dst)[N], const bool (&ok)[N],
+                                                   uint32_t lane) {
     constexpr uint32_t n16 = 8u * (FMT == kKvQ8_0 ? 34u : 18u) / 16u;
-    const uint32_t r = lane >= n16 ? 1u : 0u, c = lane - r * n16;
+    static_assert(N * n16 <= 64, "one 16-byte chunk per lane");
+    const uint32_t r = N == 1 ? 0u : min(lane / n16, static_cast<uint32_t>(N - 1)), c = lane - r * n16;
+    uint8_t* d = dst[0];
+    bool o = ok[0];
+#pragma unroll
+    for (int i = 1; i < N; ++i) {
+        d = r == static_cast<uint32_t>(i) ? dst[i] : d;
+        o = r == static_cast<uint32_t>(i) ? ok[i] : o;
+    }
     PendingStore st;
-    st.addr = (global_f32x4*)(r ? dst[1] : dst[0]) + c;
-    st.data = reinterpret_cast<const f32x4*>(lds)[min(lane, 2 * n16 - 1)];
-    if (lane < 2 * n16 && (r ? ok[1] : ok[0])) __builtin_nontemporal_store(st.data, st.addr);
+    st.addr = (global_f32x4*)d + c;
+    st.data = reinterpret_cast<const f32x4*>(lds)[min(lane, N * n16 - 1)];
+    if (lane < N * n16 && o) __builtin_nontemporal_store(st.data, st.addr);
     return st;
 }
 
@@ -514,95 +527,108 @@ __global__ __launch_bounds__(256) void kv_append_row_kernel(KvAppendArgs a) {
     store_row<FMT, V4>(x, dst, rowbuf[wave], lane, kRowBytes);
 }
 
-// V-norm appends of many tokens at kv_width 256: eight tokens per
-// workgroup, two per wavefront, and a fifth wavefront whose lanes 0..7 fold
-// the eight V rows' squares in index order in one instruction stream (each
+// V-norm appends of many tokens at kv_width 256: NW worker wavefronts of TW
+// tokens each per workgroup, and one more wavefront whose lanes 0 .. NW*TW-1
+// fold the V rows' squares in index order in one instruction stream (each
 // lane's fold is the per-token kernel's, so the bits are the same) while
-// the four others encode and store their K rows and take their V rows'
-// block maxima; the V rows are scaled and encoded once their inverse RMS is
+// the workers encode and store their K rows and take their V rows' block
+// maxima; the V rows are scaled and encoded once their inverse RMS is
 // published.  A token at a position past the capacity (or past the last
 // token) stores nothing.
-constexpr uint32_t kRows8Threads = 5 * kWave;
+template <int TW, int NW>
+struct RowsShape {
+    static constexpr uint32_t kTokens = TW * NW;
+    static constexpr uint32_t kThreads = (NW + 1) * kWave;
+};
 
-template <int FMT>
-__global__ __launch_bounds__(kRows8Threads) void kv_append_rows8_kernel(KvAppendArgs a) {
+template <int FMT, int TW, int NW>
+__global__ __launch_bounds__((NW + 1) * 64) void kv_append_rows_kernel(KvAppendArgs a) {
     constexpr uint32_t kW = 256;
+    constexpr uint32_t kTok = RowsShape<TW, NW>::kTokens;
     constexpr uint32_t kRowBytes = FMT == kKvF32 ? kW * 4 : (kW / 32) * (FMT == kKvQ8_0 ? 34u : 18u);
-    // V squares, one row per token; a 65-float4 stride puts the eight rows
-    // that lanes 0..7 read together on distinct LDS banks
-    __shared__ __align__(16) f32x4 sq[8][65];
-    __shared__ float inv_lds[8];
-    __shared__ __align__(16) uint8_t rowbuf[4][FMT == kKvF32 ? 16 : 4 * kRowBytes];  // K0 K1 V0 V1
+    // V squares, one row per token; a 65-float4 stride puts the rows that
+    // the folding lanes read together on distinct LDS banks
+    __shared__ __align__(16) f32x4 sq[kTok][65];
+    __shared__ float inv_lds[kTok];
+    __shared__ __align__(16) uint8_t rowbuf[NW][FMT == kKvF32 ? 16 : 2 * TW * kRowBytes];  // K rows, then V rows
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
-    const bool folder = wave == 4;
-    const uint32_t tb = blockIdx.x * 8u + 2u * (folder ? 0u : wave);  // this wavefront's tokens tb, tb + 1
-    f32x4 k[2], v[2];
-    bool ok[2] = {false, false};
-    uint8_t* kdst[2];
-    uint8_t* vdst[2];
+    const bool folder = wave == NW;
+    const uint32_t tb = blockIdx.x * kTok + TW * (folder ? 0u : wave);  // this wavefront's tokens tb .. tb + TW - 1
+    f32x4 k[TW], v[TW];
+    bool ok[TW];
+    uint8_t* kdst[TW];
+    uint8_t* vdst[TW];
     if (!folder) {
         // Vector loads return in issue order, so a wait for one load waits
-        // for every load issued before it.  Issue order: the two positions
+        // for every load issued before it.  Issue order: the positions
         // (needed first, for the store addresses), the V rows (the fold
         // waits only for them), then the K rows, which arrive while the
         // fold runs.
-        uint32_t position[2];
+        uint32_t position[TW];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) position[i] = a.positions[min(tb + i, a.tokens - 1)];
+        for (int i = 0; i < TW; ++i) position[i] = a.positions[min(tb + i, a.tokens - 1)];
         __asm__ volatile("" ::: "memory");
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < TW; ++i) {
             const size_t t = min(tb + i, a.tokens - 1);  // loads of a token past the end are clamped, never stored
             v[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a.value + t * kW) + lane);
         }
         __asm__ volatile("" ::: "memory");
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < TW; ++i) {
             const size_t t = min(tb + i, a.tokens - 1);
             k[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(a.key + t * kW) + lane);
         }
         __asm__ volatile("" ::: "memory");
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < TW; ++i) {
             ok[i] = tb + i < a.tokens && position[i] < a.capacity;
             const uint32_t p = ok[i] ? position[i] : 0u;  // no address is formed past the cache
             kdst[i] = a.cache + static_cast<size_t>(p) * kRowBytes;
             vdst[i] = a.cache + (static_cast<size_t>(a.capacity) + p) * kRowBytes;
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            sq[2 * wave + i][lane] = f32x4{v[i].x * v[i].x, v[i].y * v[i].y, v[i].z * v[i].z, v[i].w * v[i].w};
+        for (int i = 0; i < TW; ++i)
+            sq[TW * wave + i][lane] = f32x4{v[i].x * v[i].x, v[i].y * v[i].y, v[i].z * v[i].z, v[i].w * v[i].w};
     }
     __syncthreads();
-    float vmax[2] = {0.0f, 0.0f};
+    float vmax[TW];
     PendingStore kstore;
     if (folder) {
-        if (lane < 8)
+        if (lane < kTok)
             inv_lds[lane] = inverse_rms(fold_lds_chunk(sq[lane], 64u, 0.0f), static_cast<float>(kW), a.epsilon);
     } else if (FMT == kKvF32) {
-        const float one[2] = {1.0f, 1.0f};
-        store_f32_rows2<false>(k, one, kdst, ok, lane);
+        float one[TW];
+#pragma unroll
+        for (int i = 0; i < TW; ++i) one[i] = 1.0f;
+        store_f32_rows<TW, false>(k, one, kdst, ok, lane);
     } else {
         // while the fold runs: the K rows are encoded and stored (their
         // writes overlap the fold), and the V rows' block maxima are taken
-        const float one[2] = {1.0f, 1.0f};
-        const float kmax[2] = {block_max(k[0]), block_max(k[1])};
-        encode_rows2<FMT, false>(k, one, kmax, rowbuf[wave], lane);
-        lds_wave_handoff();
-        kstore = flush_rows2<FMT>(rowbuf[wave], kdst, ok, lane);
+        float one[TW], kmax[TW];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) vmax[i] = block_max(v[i]);
+        for (int i = 0; i < TW; ++i) {
+            one[i] = 1.0f;
+            kmax[i] = block_max(k[i]);
+        }
+        encode_rows<FMT, TW, false>(k, one, kmax, rowbuf[wave], lane);
+        lds_wave_handoff();
+        kstore = flush_rows<FMT, TW>(rowbuf[wave], kdst, ok, lane);
+#pragma unroll
+        for (int i = 0; i < TW; ++i) vmax[i] = block_max(v[i]);
     }
     __syncthreads();
     if (folder) return;
-    const float inv[2] = {inv_lds[2 * wave], inv_lds[2 * wave + 1]};
+    float inv[TW];
+#pragma unroll
+    for (int i = 0; i < TW; ++i) inv[i] = inv_lds[TW * wave + i];
     if (FMT == kKvF32) {
-        store_f32_rows2<true>(v, inv, vdst, ok, lane);
+        store_f32_rows<TW, true>(v, inv, vdst, ok, lane);
     } else {
-        encode_rows2<FMT, true>(v, inv, vmax, rowbuf[wave] + 2 * kRowBytes, lane);
+        encode_rows<FMT, TW, true>(v, inv, vmax, rowbuf[wave] + TW * kRowBytes, lane);
         lds_wave_handoff();
-        flush_rows2<FMT>(rowbuf[wave] + 2 * kRowBytes, vdst, ok, lane);
+        flush_rows<FMT, TW>(rowbuf[wave] + TW * kRowBytes, vdst, ok, lane);
         keep_alive(kstore);
     }
 }
@@ -615,7 +641,17 @@ bool launch_row(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
     if ((w != 256 && w != 512 && w != 1024) || !aligned16(a.key) || !aligned16(a.value) || !aligned16(a.cache))
         return false;
     if (vnorm && w == 256 && a.tokens >= 256) {
-        hipLaunchKernelGGL((kv_append_rows8_kernel<FMT>), dim3((a.tokens + 7) / 8), dim3(kRows8Threads), 0, stream, a);
+        // Tokens per worker wavefront (TW) and workers per workgroup (NW),
+        // measured on MI355X at 4096 tokens into a 4096-position cache
+        // (TW x NW: f32 / Q8_0 / Q4_0 us): 2x4 4.28 / 5.05 / 5.45, 1x4
+        // 4.39 / 4.78 / 4.89, 1x8 4.41 / 4.84 / 4.95, 2x2 4.37 / 5.11 / 5.49,
+        // 1x2 4.71 / 5.28 / 5.38, 2x8 4.43 / 5.16 / 5.47.  The encoders'
+        // V rows wait for the fold, so one row per worker shortens the chain
+        // after it; the f32 rows only scale and store.
+        constexpr int kTw = FMT == kKvF32 ? 2 : 1;
+        using Shape = RowsShape<kTw, 4>;
+        hipLaunchKernelGGL((kv_append_rows_kernel<FMT, kTw, 4>), dim3((a.tokens + Shape::kTokens - 1) / Shape::kTokens),
+                           dim3(Shape::kThreads), 0, stream, a);
         return true;
     }
     const dim3 grid((a.tokens + 1) / 2);

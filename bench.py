@@ -590,8 +590,10 @@ def floor_fields(floor, nbytes, out_bytes, op_us, iters):
     """floor_us: the size-matched streaming floor; of_floor = floor_us / op_us
     (1.0 = the op moves its bytes as fast as a plain stream of the same size)."""
     out_bytes = min(out_bytes, nbytes)
-    fu = floor.us(nbytes - out_bytes, out_bytes, iters)
-    return {"floor_us": round(fu, 3), "of_floor": round(fu / op_us, 4)}
+    kinds = floor.us_kinds(nbytes - out_bytes, out_bytes, iters)
+    fu = min(kinds.values())
+    return {"floor_us": round(fu, 3), "of_floor": round(fu / op_us, 4),
+            "floor_us_by_kind": [round(kinds[k], 3) for k in sorted(kinds)]}
 
 
 def floor_sweep(rt, iters):

@@ -95,9 +95,9 @@ def _values(r, tokens, w, kind):
                                           (32, 9, 16), (4096, 3, 4), (96, 33, 40), (1024, 130, 128)])
 @pytest.mark.parametrize("kind", ["normal", "adversarial", "nan", "band"])
 def test_kv_append_shapes(rt, ora, fmt, w, tokens, cap, kind):
-    """Decode (one token at a random position), prefill batches (eight tokens
-    per workgroup with the V norm at width 256, a ragged last workgroup at
-    301 tokens), ragged widths,
+    """Decode (one token at a random position), prefill batches (eight f32 /
+    four quantised tokens per workgroup with the V norm at width 256, a
+    ragged last workgroup at 301 tokens), ragged widths,
     positions past the capacity (skipped), adversarial blocks, NaN blocks
     and rows (the encoders' maximum starts at 0, as the reference's does),
     and quotients at and beside half-integers (the exact recompute)."""
