@@ -576,6 +576,17 @@ __device__ __forceinline__ float wave_sum_tree_f32(float v) {
     return readlane_f32(v, 0) + readlane_f32(v, 32);
 }
 
+// Maximum over the wavefront by the same DPP / swizzle steps (fmaxf: exact in
+// any order; NaN lanes never win over a number), the result in every lane.
+__device__ __forceinline__ float wave_max_tree_f32(float v) {
+    v = fmaxf(v, dpp_f32<0xb1, 0xf, false>(v));
+    v = fmaxf(v, dpp_f32<0x4e, 0xf, false>(v));
+    v = fmaxf(v, dpp_f32<0x141, 0xf, false>(v));
+    v = fmaxf(v, dpp_f32<0x140, 0xf, false>(v));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401f)));
+    return fmaxf(readlane_f32(v, 0), readlane_f32(v, 32));
+}
+
 __device__ __forceinline__ float wave_sum_any_order_f32(float v) {
     v += dpp_f32<0x111, 0xf, true>(v);
     v += dpp_f32<0x112, 0xf, true>(v);

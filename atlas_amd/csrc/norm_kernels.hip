@@ -810,6 +810,8 @@ __global__ __launch_bounds__(64) void groups_stable_kernel(float* values, const 
 // Groups of width <= 64 * PER: the same steps with the group and its norm
 // weights held in registers (lane l: values l + 64k), one read and one write
 // of global memory; the sequential fold stages the squares in LDS as above.
+// The maximum and the tree sum take DPP steps (no LDS round trips): the
+// PLE projection's norm launch, 35 groups of 256, is latency alone.
 template <int PER>
 __global__ __launch_bounds__(64) void groups_stable_reg_kernel(float* values, const float* weight, uint32_t width,
                                                                float epsilon, int sequential) {
@@ -825,7 +827,7 @@ __global__ __launch_bounds__(64) void groups_stable_reg_kernel(float* values, co
         w[k] = i < width ? weight[i] : 0.0f;
         m = fmaxf(m, fabsf(x[k]));
     }
-    m = wave_max(m);
+    m = wave_max_tree_f32(m);
     if (m == 0.0f) {
 #pragma unroll
         for (int k = 0; k < PER; ++k)
@@ -859,7 +861,7 @@ __global__ __launch_bounds__(64) void groups_stable_reg_kernel(float* values, co
         __syncthreads();
         sum = total;
     } else {
-        sum = wave_sum(partial);
+        sum = wave_sum_tree_f32(partial);
     }
     const float root = sqrt_rn(fdiv_rn(sum, static_cast<float>(width)) + fdiv_rn(epsilon, m * m));
     const float inv = fdiv_rn(fdiv_rn(1.0f, root), m);
