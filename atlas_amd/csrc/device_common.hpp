@@ -28,19 +28,18 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // Store cache policies (gfx950 buffer-instruction bits: sc0 = 1, nt = 2,
-// sc1 = 16).  Both system-scope policies write the line through to memory at
-// once instead of leaving it dirty in L2, so the kernel's end has no
-// write-back left to drain; they pay where a kernel's bytes are mostly
-// written and cost where reads dominate (QK-norm + RoPE 15.6 against 14.3 us
-// with nontemporal stores, RMSNorm 9.4 against 8.8, GeGLU 49.5 against 47.8).
-// Which of the two wins depends on the kernel, measured on MI355X at 4096
-// tokens: the quantised token gathers (7 bytes written per byte read) take
-// kPolicySystem (Q4_0 4.99 us, 5.25 with kPolicyWriteThrough, 5.74 with
-// nontemporal stores); the PLE gather, which also streams the projection in,
-// takes kPolicyWriteThrough (47.7 us, 56.6 with kPolicySystem).
+// sc1 = 16).  kPolicyWriteThrough = sc0 | sc1 | nt: system-scope,
+// nontemporal -- the line is written through to memory at once instead of
+// staying dirty in L2, so the kernel's end has no write-back left to drain.
+// It pays where a kernel's bytes are mostly written (the token gathers write
+// 7 bytes per byte read: Q4_0 at T = 4096 5.25 against 5.74 us with
+// nontemporal stores); where reads dominate it costs (QK-norm + RoPE 15.4
+// against 14.2 us, RMSNorm 9.4 against 8.8, GeGLU 49.5 against 47.8).
+// sc0 | sc1 without nt timed faster per gather launch (4.99 against 5.25 us)
+// but made the seven-op T = 4096 step 10.6 us slower (155.8 against 145.2):
+// its writes are still draining while the next op runs.
 constexpr int kPolicyNt = 2;
-constexpr int kPolicySystem = 17;        // sc0 | sc1
-constexpr int kPolicyWriteThrough = 19;  // sc0 | sc1 | nt
+constexpr int kPolicyWriteThrough = 19;
 
 // Buffer resource over `bytes` from a wavefront-uniform `base` (raw
 // buffer, no swizzle): stores through it at a per-lane byte offset.

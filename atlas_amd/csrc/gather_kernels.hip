@@ -251,7 +251,7 @@ __global__ __launch_bounds__(64 * WPG) void embed_quant_kernel(const uint8_t* __
             q8_0_decode4(pass, lane * 4, v);
         else
             q4_0_decode4(pass, lane * 4, v);
-        st_span4<kPolicySystem>(ro, 4u * c, f32x4{v[0] * scale, v[1] * scale, v[2] * scale, v[3] * scale});
+        st_span4<kPolicyWriteThrough>(ro, 4u * c, f32x4{v[0] * scale, v[1] * scale, v[2] * scale, v[3] * scale});
         pass += kPassBytes;
     }
 }
@@ -372,8 +372,6 @@ hipError_t launch_embed_fmt(hipStream_t stream, const uint8_t* table, const uint
     // 1536; sc0|sc1|nt stores, host-selected staging unit): Q4_0 5.09 us
     // with one, 5.12 with two, 5.19 with four, 5.20-5.25 with eight or
     // sixteen; Q6_K 5.42 us with two, 5.51-5.58 with one, 5.46 with four.
-    // With the sc0|sc1 stores now used Q6_K measures the same with two or
-    // four (5.44-5.46 us).
     // Decode batches take one (256 tokens spread over 256 CUs), and so do
     // rows whose two slots would not fit 64 KiB of LDS.
     const bool two = FMT != kQuantQ4_0 && tokens >= 2048 && 2u * quant_slot_bytes(FMT, hidden) <= 65536u;
