@@ -471,10 +471,19 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
 
     float s = 0.0f;  // lane r < nrows: running sum of squares of row r
     uint32_t sb[R];  // PAR: running sums of squares (bit patterns, wave-uniform)
+    // In-order engine (!PAR): the row's last chunk takes the exact
+    // wave-parallel fold instead (one per row, after the in-order chunks):
+    // the later chunks of a row land together, and the last one's in-order
+    // adds would run after the read window closes.  Measured on MI355X at
+    // [4096, 1536], residual: 13.68 against 13.98 us; the last two chunks
+    // 13.90, the last three 13.98, every chunk after the first 14.9.
+    constexpr int kTailN = 1;
+    constexpr bool kTail = !PAR && J > 1;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const uint32_t creal = lane + 64u * j;
         const uint32_t c = min(creal, nv - 1);
+        const bool par_chunk = PAR ? j > 0 : (kTail && j >= J - kTailN);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             f32x4 v = x[r][j];
@@ -483,7 +492,7 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
                 v = f32x4{v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w};
                 x[r][j] = v;
             }
-            if (!PAR || j == 0) {
+            if (!par_chunk) {
                 sq4[r * stride4 + c] = f32x4{v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w};
             } else if (kRun) {
                 // staged for the one-step continuation below (+0 past the row
@@ -499,12 +508,12 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
                 sb[r] = fold_chunk_exact<4>(sq, sb[r]);
             }
         }
-        if ((!PAR || j == 0) && !kRun) {
+        if (!par_chunk && !kRun) {
             __syncthreads();
             if (lane < nrows)
                 s = fold_lds_chunk(sq4 + lane * stride4 + 64u * j, min(nv, 64u * (j + 1)) - 64u * j, s);
         }
-        if (PAR && !kRun && j == 0) {
+        if ((PAR && !kRun && j == 0) || (kTail && j == J - kTailN - 1)) {
             // the first chunk, where the sum crosses many binades and ties are
             // frequent, folds in order; broadcast each row's partial sum
 #pragma unroll
@@ -553,7 +562,7 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         if (static_cast<uint32_t>(r) >= nrows) break;
-        const float ir = PAR ? inverse_rms(__uint_as_float(sb[r]), static_cast<float>(h), a.epsilon)
+        const float ir = (PAR || kTail) ? inverse_rms(__uint_as_float(sb[r]), static_cast<float>(h), a.epsilon)
                              : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
         const size_t base = static_cast<size_t>(row0 + r) * h;
         f32x4 n[J];
@@ -601,7 +610,9 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
 //    ([4096, 1536]: 11.7 -> 10.6 us);
 //  * rows >= 2048 with an epilogue operand (residual, add-norm, add-scale):
 //    two rows per wavefront (two wavefronts per SIMD) and the in-order fold
-//    ([4096, 1536] residual: 16.0 us; one row and the parallel fold: 16.7).
+//    up to the last chunk ([4096, 1536] residual: 16.0 us; one row and the
+//    parallel fold: 16.7; two rows with the parallel fold after the first
+//    chunk, on the later engine: 14.9 against 13.7).
 struct RegConfig {
     int rows;
     bool par;
