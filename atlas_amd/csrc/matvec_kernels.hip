@@ -224,14 +224,22 @@ __global__ __launch_bounds__(256) void q4_0_matvec_kernel(MatvecArgs a) {
     }
     ss = group_sum<kWave>(ss);
     if (lane == 0) partial[wave] = ss;
+    // y, the block sums and the partial sums are shared; the weight rows are
+    // the wavefront's own, so it waits for its rows alone and starts its dot
+    // while the workgroup's other rows may still be in flight (gate/up at
+    // one token: 5.30 against 5.39 us with the rows written before the
+    // barrier)
+    __syncthreads();
     if constexpr (ONEPASS) {
         u32x4* dst = reinterpret_cast<u32x4*>(tile + wrow0 * row_bytes);
         dst[min(lane, n16 - 1)] = w0;
         dst[min(lane + kWave, n16 - 1)] = w1;
         dst[min(lane + 2 * kWave, n16 - 1)] = w2;
         dst[min(lane + 3 * kWave, n16 - 1)] = w3;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    __syncthreads();
     // The projection is held to a tolerance (this kernel's own summation
     // order), so the inverse RMS takes the hardware reciprocal and reciprocal
     // square root (each within 1 ulp): rsq(sum * rcp(n) + eps), a few ulp,
