@@ -26,7 +26,9 @@
 // The f32 arithmetic is IEEE (correctly rounded division and sqrt).
 //
 // Layout on CDNA: for kv_width 256, 512 or 1024 with 16-byte aligned rows,
-// one wavefront per token (kv_append_row_kernel, below).  Otherwise one
+// one wavefront per token (kv_append_row_kernel, below); with the V norm at
+// width 256 and at least 256 tokens, worker wavefronts beside one that folds
+// every V row of the workgroup (kv_append_rows_kernel).  Otherwise one
 // 256-thread workgroup per token: thread t owns values t + 256p of the K and
 // V rows; a 32-value block is exactly half a wavefront, so block maxima are
 // half-wave reductions (DPP steps and one ds_swizzle) and the Q4_0 nibble
