@@ -744,16 +744,25 @@ __global__ __launch_bounds__(256) void rope_half_token_kernel(const uint8_t* x0,
     float cs[V], sn[V];
     ld_tab<V>(cosine + static_cast<size_t>(t) * rope_stride + g * V, cs);
     ld_tab<V>(sine + static_cast<size_t>(t) * rope_stride + g * V, sn);
-    auto head_offset = [&](uint32_t h, bool second) -> size_t {
-        return (second ? static_cast<size_t>(t) * heads1 + (h - heads0) : static_cast<size_t>(t) * heads0 + h) *
-                   row_bytes + vec * 16u;
-    };
+    // Both halves as one form, y = own*c + par*s' with s' = -s on the first
+    // half's lanes: x0*c - x1*s is x0*c + x1*(-s) (IEEE subtraction adds the
+    // negation, and round-to-nearest is symmetric in sign, so fl(x1*(-s)) =
+    // -fl(x1*s), zeros included), and x0*s + x1*c is x1*c + x0*s (addition
+    // commutes).  No per-value select between the halves' formulas.
+#pragma unroll
+    for (int j = 0; j < static_cast<int>(V); ++j) sn[j] = first ? -sn[j] : sn[j];
+    // row offset of head step i (clamped to a valid head for the load; a step
+    // past the last head is never stored, so the store reuses the offset)
+    size_t off[NI];
+    bool sec[NI];
     u32x4r v[NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
         const uint32_t h = min(hl + static_cast<uint32_t>(i) * hps, heads - 1);
-        const bool second = h >= heads0;
-        v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4r*>((second ? x1 : x0) + head_offset(h, second)));
+        sec[i] = h >= heads0;
+        off[i] = (sec[i] ? static_cast<size_t>(t) * heads1 + (h - heads0) : static_cast<size_t>(t) * heads0 + h) *
+                     row_bytes + vec * 16u;
+        v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4r*>((sec[i] ? x1 : x0) + off[i]));
     }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -762,29 +771,22 @@ __global__ __launch_bounds__(256) void rope_half_token_kernel(const uint8_t* x0,
         uint32_t par[4];
 #pragma unroll
         for (int w = 0; w < 4; ++w) par[w] = rope_partner<GSH>(own[w], G);
-        const uint32_t h = hl + static_cast<uint32_t>(i) * hps;
-        if (h < heads) {
-            const bool second = h >= heads0;
+        if (hl + static_cast<uint32_t>(i) * hps < heads) {
             u32x4r r;
             uint32_t* o = reinterpret_cast<uint32_t*>(&r);
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                const uint32_t wa = first ? own[w] : par[w], wb = first ? par[w] : own[w];
                 if constexpr (F16) {
                     // each product rounded once (the f16 operand widens inside
-                    // the multiply), then the sum or difference
-                    const float c0 = cs[2 * w], c1 = cs[2 * w + 1], s0 = sn[2 * w], s1 = sn[2 * w + 1];
-                    const float pa0 = mul_f16_half<0>(first ? c0 : s0, wa), pb0 = mul_f16_half<0>(first ? s0 : c0, wb);
-                    const float pa1 = mul_f16_half<1>(first ? c1 : s1, wa), pb1 = mul_f16_half<1>(first ? s1 : c1, wb);
-                    const float y0 = first ? pa0 - pb0 : pa0 + pb0;
-                    const float y1 = first ? pa1 - pb1 : pa1 + pb1;
+                    // the multiply), then the sum
+                    const float y0 = mul_f16_half<0>(cs[2 * w], own[w]) + mul_f16_half<0>(sn[2 * w], par[w]);
+                    const float y1 = mul_f16_half<1>(cs[2 * w + 1], own[w]) + mul_f16_half<1>(sn[2 * w + 1], par[w]);
                     o[w] = static_cast<uint32_t>(f2h(y0)) | (static_cast<uint32_t>(f2h(y1)) << 16);
                 } else {
-                    const float xa = __uint_as_float(wa), xb = __uint_as_float(wb);
-                    o[w] = __float_as_uint(first ? xa * cs[w] - xb * sn[w] : xa * sn[w] + xb * cs[w]);
+                    o[w] = __float_as_uint(__uint_as_float(own[w]) * cs[w] + __uint_as_float(par[w]) * sn[w]);
                 }
             }
-            __builtin_nontemporal_store(r, reinterpret_cast<u32x4r*>((second ? out1 : out0) + head_offset(h, second)));
+            __builtin_nontemporal_store(r, reinterpret_cast<u32x4r*>((sec[i] ? out1 : out0) + off[i]));
         }
     }
 }

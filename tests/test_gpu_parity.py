@@ -571,3 +571,46 @@ def test_swiglu_f16_zero_signs_and_specials(rt, ora):
     # the zero products keep their signs
     zero = (e16 & 0x7fff) == 0
     assert zero.sum() > 100 and np.array_equal(g16[zero], e16[zero])
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_rope_half_token_engine_signed_zeros_and_specials(rt, ora, f16, head_dim):
+    """The token engine takes both halves as own*c + par*s', s' = -s on the
+    first half's lanes: bit-identical to the reference's x0*c - x1*s and
+    x0*s + x1*c for every finite input, signed zeros included -- rows of +-0 in
+    either half (all four sign pairs), at position 0 (cos 1, sin 0) and at
+    other positions -- and NaN where the reference gives NaN (infinities,
+    NaN; compared NaN-equal).  f16 at head_dim 64 / 128 and f32 at 64 take the
+    two mirrored DPP layouts, f32 at 128 the shuffle exchange."""
+    tokens, heads = 2048, 8
+    half = head_dim // 2
+    r = wl.rng(4242 + head_dim + f16)
+    x = wl.normal(r, tokens * heads * head_dim).reshape(tokens, heads, 2, half)
+    zero_pairs = [(0.0, 0.0), (-0.0, 0.0), (0.0, -0.0), (-0.0, -0.0)]
+    for i, (a, b) in enumerate(zero_pairs):
+        x[i::16, :, 0, :] = a           # rows of position 0 and later ones
+        x[i::16, :, 1, :] = b
+    x[4::16, :, 1, :] = -0.0            # one half zero, the other normal
+    x[5::16, :, 0, :] = -0.0
+    x[6::16, :, 0, ::3] = np.inf
+    x[7::16, :, 1, 1::3] = -np.inf
+    x[8::16, :, 0, 2::5] = np.nan
+    x[9::16, :, 1, ::7] = np.nan
+    x = x.reshape(-1).astype(np.float32)
+    if f16:
+        x = x.astype(np.float16).view(np.uint16)
+    inp, m = {"x": x, "pos": np.arange(tokens, dtype=np.uint32)}, dict(
+        tokens=tokens, heads=heads, head_dim=head_dim, theta=130000.0, f16=f16)
+    say(f"rope_half specials f16={f16} head_dim={head_dim}")
+    got = cases.rope_half_gpu(rt, inp, m, rope_tables_llama(inp["pos"], head_dim, 130000.0))[0]
+    exp = cases.rope_half_oracle(ora, inp, m)[0]
+    if f16:
+        g, e = got.view(np.float16), exp.view(np.float16)
+        same = (got == exp) | (np.isnan(g) & np.isnan(e))
+        assert same.all(), f"{int((~same).sum())} differ; first at {int(np.nonzero(~same)[0][0])}"
+        zero = (exp & 0x7fff) == 0
+    else:
+        assert_bits_nan_equal("rope_half specials", [got], [exp])
+        zero = (exp.view(np.uint32) & 0x7fffffff) == 0
+    assert zero.sum() > 1000 and np.signbit(exp[zero].view(np.float16 if f16 else np.float32)).any()
