@@ -178,12 +178,13 @@ def run_prefill(rt, ora, ch, tree_norms):
         ch.close()
 
 
-def test_gemma_prefill_chunk_eager_and_graph_replays(rt, ora):
+@pytest.mark.parametrize("kv_format", ["q8_0", "q4_0"])
+def test_gemma_prefill_chunk_eager_and_graph_replays(rt, ora, kv_format):
     """T = 512 tokens, five layers (four sliding-window, one full; the last
-    reads an earlier layer's KV, so it has no K head), Q8_0 KV cache with the
-    fused V norm; chunk A at positions 0-511, then replays of chunks B
-    (512-1023), A and B."""
-    run_prefill(rt, ora, GemmaPrefillChunk(rt, PrefillShape(), kv_format="q8_0"), tree_norms=False)
+    reads an earlier layer's KV, so it has no K head), a Q8_0 or Q4_0 KV cache
+    with the fused V norm; chunk A at positions 0-511, then replays of chunks
+    B (512-1023), A and B."""
+    run_prefill(rt, ora, GemmaPrefillChunk(rt, PrefillShape(), kv_format=kv_format), tree_norms=False)
 
 
 def test_gemma_prefill_chunk_under_auto_reduction(rt_auto, ora):
