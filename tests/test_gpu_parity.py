@@ -446,8 +446,8 @@ def test_wide_reduction_is_tolerance_level(rt, ora):
         rt.set_reduction(ATLAS_REDUCTION_SEQUENTIAL)
 
 
-@pytest.mark.parametrize("rows", [2048 + 48, 1024 + 16])
-@pytest.mark.parametrize("hidden", [1536, 2048, 576, 1024, 260])
+@pytest.mark.parametrize("rows", [2048 + 48, 2048 + 47, 1024 + 16])
+@pytest.mark.parametrize("hidden", [1536, 2048, 576, 1024, 260, 1280, 1792])
 @pytest.mark.parametrize("mode", ["plain", "residual", "addnorm", "addscale"])
 def test_rms_exact_fold_adversarial_rows(rt, ora, rows, hidden, mode):
     """Both folds of the register engine against the oracle's sequential sum on
@@ -456,7 +456,9 @@ def test_rms_exact_fold_adversarial_rows(rt, ora, rows, hidden, mode):
     scans computed ahead by a helper wavefront (the walk across binade
     crossings, ties, subnormal, inf and NaN stretches); from 2048 rows up, plain
     RMSNorm keeps the chunked parallel fold and the epilogue modes fold in order
-    with two rows per wavefront (and a ragged tail)."""
+    with two rows per wavefront up to the last chunk, which takes the parallel
+    fold (2 to 8 chunks per row; an odd row count leaves the last wavefront
+    one row)."""
     inp, m = cases.rms_case(rows, hidden, 1e-6, 4000 + hidden, mode)
     inp["x"] = cases.adversarial_rows(rows, hidden, 5000 + hidden)
     say(f"rms exact fold adversarial {mode} rows={rows} hidden={hidden}")
