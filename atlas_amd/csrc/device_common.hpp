@@ -309,7 +309,11 @@ __device__ __forceinline__ float mul_f16_half(float a, uint32_t pair) {
 // keep it that way: left alone, the scheduler interleaves each read just
 // one float4 ahead of its adds, and the chain then waits on LDS latency
 // (one wavefront on gfx950: 8.7 cycles per add, 6.6 with the barriers; a
-// register-fed chain is 5.6).
+// register-fed chain is 5.6).  The schedule holds with the groups written
+// out here: the same loop moved into a template helper compiled to all reads
+// hoisted ahead of the adds, spilled to AGPRs (QK-norm + RoPE at 4096 tokens
+// 21.6 us against 14.2, the residual epilogue 20.1 against 13.7); check the
+// ISA after any change to this function.
 __device__ __forceinline__ float fold_lds_chunk(const f32x4* p, uint32_t n4, float s) {
     if (n4 == 64) {
         f32x4 cur[8], nxt[8];
