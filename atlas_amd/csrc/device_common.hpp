@@ -374,7 +374,11 @@ __device__ __forceinline__ float fold_lds_chunk(const f32x4* p, uint32_t n4, flo
 //    two (K = 2^24 - k ulps away), or that holds a tie or an out-of-range
 //    addend, is an event: the lanes before it are applied as one integer add,
 //    the event lane's S values are folded one by one in f32, and the scan is
-//    reused (same binade) or recomputed (new binade).
+//    reused (same binade) or recomputed (new binade).  Every lane folds its
+//    own S values from the start it would have as the event lane (the sum
+//    plus its exclusive prefix), which is exact for the real event lane, and
+//    one readlane takes that lane's result: the add chain does not wait for
+//    the event lane to be known, and no values move between lanes.
 //  * Sums outside [2^-100, 2^125), inf and NaN fold lane by lane in f32.
 //
 // Every step either is the sequential fold's own f32 add or provably equals
@@ -435,21 +439,23 @@ __device__ __forceinline__ uint32_t fold_chunk_exact_from(const float (&v)[S], u
         const uint64_t badmask = __builtin_amdgcn_ballot_w64(bad);
         uint32_t base = l0 ? readlane_u32(incl, l0 - 1) : 0u;
         for (;;) {
+            // every lane from its start as the event lane (lanes [l0, lc)
+            // stay in the binade, so lane lc's start is exact); issued ahead
+            // of the event search, which it does not depend on
+            float s = __uint_as_float(sb + (incl - inc) - base);
+#pragma unroll
+            for (int i = 0; i < S; ++i) s = s + v[i];
             const uint32_t room = 0x800000u - (sb & 0x7fffffu);  // ulps to the next power of two
             const uint64_t ev = (__builtin_amdgcn_ballot_w64(incl - base >= room) | badmask) & (~0ull << l0);
+            __asm__ volatile("" ::"v"(s));  // keep the chain ahead of the branch
             if (ev == 0) {
                 sb += readlane_u32(incl, 63) - base;
                 l0 = 64;
                 break;
             }
             const uint32_t lc = static_cast<uint32_t>(__builtin_ctzll(ev));
-            const uint32_t incl_lc = readlane_u32(incl, lc);
-            sb += incl_lc - readlane_u32(inc, lc) - base;  // lanes [l0, lc): same binade, exact
-            float s = __uint_as_float(sb);
-#pragma unroll
-            for (int i = 0; i < S; ++i) s = s + readlane_f32(v[i], lc);
-            sb = __float_as_uint(s);
-            base = incl_lc;
+            sb = readlane_u32(__float_as_uint(s), lc);
+            base = readlane_u32(incl, lc);
             l0 = lc + 1;
             if (l0 >= 64 || (sb >> 23) != ex) break;
         }
@@ -514,14 +520,10 @@ __device__ __forceinline__ FoldScans<NB> fold_scan_ahead(const float (&v)[S], ui
 
 // v: lane l's S consecutive addends; sb: bit pattern of the running sum
 // before them (wave-uniform).  Returns the bit pattern after all 64 * S.
-// run_lds: the same addends in LDS, lane l's at float4 (S / 4) * l, so an
-// event lane's values are read by every lane at one address (a broadcast)
-// instead of a readlane per value, whose scalar result each dependent add
-// must wait for.
+// An event folds every lane's S values from its start as the event lane
+// and takes the event lane's result (as in fold_chunk_exact_from).
 template <int S, int NB>
-__device__ __forceinline__ uint32_t fold_walk(const FoldScans<NB>& f, const float (&v)[S], uint32_t sb,
-                                              const f32x4* run_lds) {
-    static_assert(S % 4 == 0, "the LDS copy holds whole float4");
+__device__ __forceinline__ uint32_t fold_walk(const FoldScans<NB>& f, const float (&v)[S], uint32_t sb) {
     uint32_t l0 = 0;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -529,29 +531,20 @@ __device__ __forceinline__ uint32_t fold_walk(const FoldScans<NB>& f, const floa
         if (l0 >= 64 || (sb >> 23) != ex || ex < 27 || ex > 251) continue;
         uint32_t base = l0 ? readlane_u32(f.incl[b], l0 - 1) : 0u;
         for (;;) {
+            float s = __uint_as_float(sb + (f.incl[b] - f.inc[b]) - base);
+#pragma unroll
+            for (int i = 0; i < S; ++i) s = s + v[i];
             const uint32_t room = 0x800000u - (sb & 0x7fffffu);  // ulps to the next power of two
             const uint64_t ev = (__builtin_amdgcn_ballot_w64(f.incl[b] - base >= room) | f.bad[b]) & (~0ull << l0);
+            __asm__ volatile("" ::"v"(s));  // keep the chain ahead of the branch
             if (ev == 0) {
                 sb += readlane_u32(f.incl[b], 63) - base;
                 l0 = 64;
                 break;
             }
             const uint32_t lc = static_cast<uint32_t>(__builtin_ctzll(ev));
-            const uint32_t incl_lc = readlane_u32(f.incl[b], lc);
-            sb += incl_lc - readlane_u32(f.inc[b], lc) - base;  // lanes [l0, lc): same binade, exact
-            f32x4 q[S / 4];
-#pragma unroll
-            for (int k = 0; k < S / 4; ++k) q[k] = run_lds[(S / 4) * lc + k];
-            float s = __uint_as_float(sb);
-#pragma unroll
-            for (int k = 0; k < S / 4; ++k) {
-                s = s + q[k].x;
-                s = s + q[k].y;
-                s = s + q[k].z;
-                s = s + q[k].w;
-            }
-            sb = __float_as_uint(s);
-            base = incl_lc;
+            sb = readlane_u32(__float_as_uint(s), lc);
+            base = readlane_u32(f.incl[b], lc);
             l0 = lc + 1;
             if (l0 >= 64 || (sb >> 23) != ex) break;
         }

@@ -543,7 +543,7 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
         f.e0 = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(scans_lds->e0));
         float run[kRunS];
         read_run(run);
-        sb[0] = fold_walk<kRunS, 4>(f, run, __float_as_uint(head), sq4 + 64);
+        sb[0] = fold_walk<kRunS, 4>(f, run, __float_as_uint(head));
     }
     if (MODE == kNormAddNorm) {  // stored residual stream r = x + residual
 #pragma unroll
