@@ -447,10 +447,7 @@ __device__ __forceinline__ uint32_t fold_chunk_exact_from(const float (&v)[S], u
             for (int i = 0; i < S; ++i) s = s + v[i];
             const uint32_t room = 0x800000u - (sb & 0x7fffffu);  // ulps to the next power of two
             const uint64_t ev = (__builtin_amdgcn_ballot_w64(incl - base >= room) | badmask) & (~0ull << l0);
-            // keep the chain ahead of the branch, where it overlaps the event
-            // search (the compiler otherwise sinks it into the event path:
-            // C5 epilogues at 256 rows 4.70 against 4.75 us)
-            __asm__ volatile("" ::"v"(s));
+            __asm__ volatile("" ::"v"(s));  // keep the chain ahead of the branch
             if (ev == 0) {
                 sb += readlane_u32(incl, 63) - base;
                 l0 = 64;
@@ -539,7 +536,10 @@ __device__ __forceinline__ uint32_t fold_walk(const FoldScans<NB>& f, const floa
             for (int i = 0; i < S; ++i) s = s + v[i];
             const uint32_t room = 0x800000u - (sb & 0x7fffffu);  // ulps to the next power of two
             const uint64_t ev = (__builtin_amdgcn_ballot_w64(f.incl[b] - base >= room) | f.bad[b]) & (~0ull << l0);
-            __asm__ volatile("" ::"v"(s));  // keep the chain ahead of the branch
+            // keep the chain ahead of the branch, where it overlaps the event
+            // search (the compiler otherwise sinks it into the event path:
+            // C5 epilogues at 256 rows 4.70 against 4.75 us)
+            __asm__ volatile("" ::"v"(s));
             if (ev == 0) {
                 sb += readlane_u32(f.incl[b], 63) - base;
                 l0 = 64;
