@@ -249,8 +249,10 @@ __device__ __forceinline__ void sq_p(float* dst, const pvec<P>& x) {
 // TPW tokens per wavefront (tokens w and w + G, G = the grid's wavefront
 // count) and WPG wavefronts per workgroup; each wavefront uses its own LDS
 // region, so the handoff between the lanes that square and the lanes that
-// fold is a wavefront-scope fence, not a workgroup barrier.
-template <int P, int MAXU, int TPW, int WPG>
+// fold is a wavefront-scope fence, not a workgroup barrier.  SPLIT: a
+// token's units are spread over ceil(units / MAXU) consecutive wavefronts,
+// MAXU each (TPW = 1).
+template <int P, int MAXU, int TPW, int WPG, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
     const float* q, const float* k, const float* q_weight, const float* k_weight, const float* cosine,
     const float* sine, float* q_out, float* k_out, uint32_t tokens, uint32_t q_heads, uint32_t has_key,
@@ -262,10 +264,14 @@ __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
     float* sq = sq_all[wave];
-    const uint32_t w0 = blockIdx.x * WPG + wave;
+    static_assert(!SPLIT || TPW == 1, "a split token is one wavefront's only token");
+    const uint32_t total = q_heads + has_key;
+    const uint32_t wv = blockIdx.x * WPG + wave;
+    const uint32_t parts = SPLIT ? (total + MAXU - 1) / MAXU : 1u;
+    const uint32_t w0 = SPLIT ? wv / parts : wv;
+    const uint32_t ubase = SPLIT ? (wv - w0 * parts) * MAXU : 0u;  // the wavefront's first unit
     const uint32_t G = gridDim.x * WPG;
     if (w0 >= tokens) return;  // wavefront-uniform
-    const uint32_t total = q_heads + has_key;
     const uint32_t p0 = lane * P;
     uint32_t tok[TPW];
     uint32_t ntok = 0;
@@ -281,7 +287,7 @@ __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
         const uint32_t t = min(tok[i], tokens - 1);
 #pragma unroll
         for (int u = 0; u < MAXU; ++u) {
-            const uint32_t uu = min(static_cast<uint32_t>(u), total - 1);
+            const uint32_t uu = min(ubase + u, total - 1);
             const float* src = uu >= q_heads ? k + static_cast<size_t>(t) * D
                                              : q + (static_cast<size_t>(t) * q_heads + uu) * D;
             lo[i][u] = ld_p<P, true>(src + p0);
@@ -312,7 +318,7 @@ __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
     // lane i * MAXU + u folds unit u of the wavefront's token i, in index order
     float sum = 0.0f;
     const uint32_t li = lane / MAXU, lu = lane - li * MAXU;
-    const bool folds = li < ntok && lu < total;
+    const bool folds = li < ntok && ubase + lu < total;
     if (folds) {
         const f32x4* row = reinterpret_cast<const f32x4*>(sq + lane * STRIDE);
 #pragma unroll
@@ -328,9 +334,9 @@ __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
         const pvec<P>& s = sn[i];
 #pragma unroll
         for (int u = 0; u < MAXU; ++u) {
-            if (static_cast<uint32_t>(u) < total) {
+            if (ubase + u < total) {
                 const float iu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), i * MAXU + u));
-                const bool key = static_cast<uint32_t>(u) >= q_heads;
+                const bool key = ubase + u >= q_heads;
                 pvec<P> ol, oh;
 #pragma unroll
                 for (int j = 0; j < P; ++j) {
@@ -342,7 +348,7 @@ __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
                     oh.v[j] = x0 * s.v[j] + x1 * c.v[j];
                 }
                 float* dst = key ? k_out + static_cast<size_t>(t) * D
-                                 : q_out + (static_cast<size_t>(t) * q_heads + u) * D;
+                                 : q_out + (static_cast<size_t>(t) * q_heads + ubase + u) * D;
                 st_p<P>(dst + p0, ol);
                 st_p<P>(dst + HALF + p0, oh);
             }
@@ -374,12 +380,38 @@ hipError_t launch_qk_token_cfg(hipStream_t s, const float* q, const float* k, co
     return hipErrorInvalidValue;
 }
 
-// One token per wavefront; four wavefronts per workgroup from 2048 tokens
-// up.  Measured on MI355X at C3 (4096 tokens, 8 Q heads + K, head_dim 256):
-// 14.17 us against 14.25-14.33 with one wavefront per workgroup and 14.9-15.0
-// with two tokens per wavefront (their two folds then share one wavefront's
-// critical path).  Decode batches keep one wavefront per workgroup, so 256
-// tokens still spread over 256 CUs.
+// A token's units over ceil(units / U) wavefronts, one wavefront per workgroup.
+template <int P, int U>
+hipError_t launch_qk_split(hipStream_t s, const float* q, const float* k, const float* qw, const float* kw,
+                           const float* c, const float* sn, float* qo, float* ko, uint32_t tokens, uint32_t q_heads,
+                           uint32_t has_key, uint32_t rope_stride, float eps) {
+    const uint32_t total = q_heads + has_key;
+    const uint64_t waves = static_cast<uint64_t>(tokens) * ((total + U - 1) / U);
+    if (waves > 0x7fffffffu) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((qk_norm_rope_token_kernel<P, U, 1, 1, true>), dim3(static_cast<uint32_t>(waves)), dim3(64), 0,
+                       s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
+    return hipGetLastError();
+}
+
+// Wavefronts per token by token count.  A wavefront folds its units' rows
+// in order (lane u, unit u), a chain of 2 * P * 64 adds whatever the unit
+// count, while its loads, squares and rotations grow with the units it
+// holds; few tokens leave most CUs idle, so below 768 tokens a token's
+// units are spread over several wavefronts.  Measured on MI355X (8 Q heads
+// + K, head_dim 256, per launch over rotating buffer sets):
+//   tokens     1 unit/wave  2 units  1 token/wave  4 tokens/workgroup
+//   256          4.80        4.81      5.46          6.10 us
+//   512          5.78        5.32      6.06          6.27
+//   1024         8.32        7.45      6.62          6.51
+//   1536        10.63        9.70      7.16          7.45
+//   2047        13.00       11.07      7.88          8.00
+// and at 4096 tokens 14.17 us with four wavefronts per workgroup against
+// 14.25-14.33 with one and 18.3 with two units per wavefront.  In the C5
+// decode step (a graph of 35 launches): 256 tokens 3.86 us with two units
+// per wavefront against 4.06-4.64 with one and 4.72 with one wavefront per
+// token; one token 2.55 (one unit), 2.69 (two), 3.97 (one wavefront); 16 and
+// 128 tokens favour one unit per wavefront (2.99 against 3.16, 3.46 against
+// 3.75), 32 and 64 tie.
 template <int P>
 hipError_t launch_qk_token_p(hipStream_t s, const float* q, const float* k, const float* qw, const float* kw,
                              const float* c, const float* sn, float* qo, float* ko, uint32_t tokens,
@@ -387,7 +419,12 @@ hipError_t launch_qk_token_p(hipStream_t s, const float* q, const float* k, cons
     if (tokens >= 2048)
         return launch_qk_token_cfg<P, 1, 4>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride,
                                             eps);
-    return launch_qk_token_cfg<P, 1, 1>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
+    if (tokens >= 768)
+        return launch_qk_token_cfg<P, 1, 1>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride,
+                                            eps);
+    if (tokens >= 256)
+        return launch_qk_split<P, 2>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
+    return launch_qk_split<P, 1>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
 }
 
 // Generic head_dim fallback (even head_dim not of the form 64*V): one wave

@@ -170,9 +170,12 @@ def test_reference_fusion_parity_seeds(rt, ora):
 @pytest.mark.parametrize("head_dim,rope_stride,q_heads,has_key", [
     (256, 128, 8, True), (256, 256, 8, True), (512, 256, 8, True), (128, 64, 4, True), (256, 128, 8, False),
     (96, 48, 3, True), (64, 32, 2, True)])
-@pytest.mark.parametrize("tokens", [37, 2051])
+@pytest.mark.parametrize("tokens", [37, 300, 1000, 2051])
 def test_qk_norm_rope_shapes(rt, ora, head_dim, rope_stride, q_heads, has_key, tokens):
-    """One and four wavefronts per workgroup (2051 tokens: a ragged last workgroup)."""
+    """Each token engine: a token's units one per wavefront (37 tokens) or two
+    per wavefront (300; odd unit counts leave a last wavefront one unit), one
+    token per wavefront (1000) and four per workgroup (2051 tokens: a ragged
+    last workgroup)."""
     inp, m = cases.qk_case(tokens, q_heads, head_dim, rope_stride, 1e6, 1e-6, 500 + head_dim, has_key, start=1000)
     tables = rope_tables_gemma4(inp["pos"], rope_stride, head_dim, 1e6)
     say(f"qk_norm_rope {m}")
