@@ -120,17 +120,47 @@ __global__ __launch_bounds__(256) void geglu_offset_kernel(const float* gate, co
 // The same product, four columns per thread with 128-bit accesses: needs
 // width, ple_offset and ple_row_stride divisible by 4, 16-byte aligned
 // buffers and rows * width / 4 < 2^32 (all in float4 units below).
-__global__ __launch_bounds__(256) void geglu_offset_vec_kernel(const f32x4* gate, const f32x4* ple, f32x4* out,
-                                                               uint32_t ple_offset4, uint32_t ple_row_stride4,
-                                                               uint32_t width4, uint32_t n4) {
+template <int V>
+struct VecOf;
+template <>
+struct VecOf<1> {
+    typedef float type;
+};
+template <>
+struct VecOf<4> {
+    typedef f32x4 type;
+};
+
+template <int V>
+__global__ __launch_bounds__(256) void geglu_offset_vec_kernel(const float* gate, const float* ple, float* out,
+                                                               uint32_t ple_offset_v, uint32_t ple_row_stride_v,
+                                                               uint32_t width_v, uint32_t nv) {
+    typedef typename VecOf<V>::type vt;
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n4) return;
-    const uint32_t r = i / width4, c = i - r * width4;
-    const f32x4 g = __builtin_nontemporal_load(gate + i);
-    const f32x4 p = ple[static_cast<uint64_t>(r) * ple_row_stride4 + ple_offset4 + c];
-    float v[4] = {g.x, g.y, g.z, g.w};
+    if (i >= nv) return;
+    const uint32_t r = i / width_v, c = i - r * width_v;
+    const vt g = __builtin_nontemporal_load(reinterpret_cast<const vt*>(gate) + i);
+    const vt p = reinterpret_cast<const vt*>(ple)[static_cast<uint64_t>(r) * ple_row_stride_v + ple_offset_v + c];
+    float v[V], pv[V];
+    if constexpr (V == 1) {
+        v[0] = g;
+        pv[0] = p;
+    } else {
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            v[k] = g[k];
+            pv[k] = p[k];
+        }
+    }
     gelu_lanes(v);
-    __builtin_nontemporal_store(f32x4{v[0] * p.x, v[1] * p.y, v[2] * p.z, v[3] * p.w}, out + i);
+    vt o;
+    if constexpr (V == 1) {
+        o = v[0] * pv[0];
+    } else {
+#pragma unroll
+        for (int k = 0; k < V; ++k) o[k] = v[k] * pv[k];
+    }
+    __builtin_nontemporal_store(o, reinterpret_cast<vt*>(out) + i);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -206,12 +236,23 @@ hipError_t launch_geglu_offset_f32(hipStream_t stream, const float* gate, const 
     if (width % 4 == 0 && ple_offset % 4 == 0 && ple_row_stride % 4 == 0 && n / 4 < (1ull << 32) &&
         aligned16(gate) && aligned16(ple) && aligned16(out)) {
         // 64-thread blocks while the whole range is under 2048 full blocks, so
-        // a decode-sized range (256 rows x 256) still spreads over every CU
+        // a decode-sized range (256 rows x 256) still spreads over every CU.
+        // From 16384 values (256 wavefronts at one value per lane) up to that
+        // size, one value per lane: the GELU's dependent chain, not the bytes,
+        // bounds a decode-sized launch, and four values per lane leave three of
+        // each CU's SIMDs idle.  Measured on MI355X (C5 decode, 256 x 256):
+        // 2.24-2.25 us against 2.39 with four values per lane and 2.26 with two;
+        // one row (256 values) 1.78 with four against 1.86-1.87.
         const uint32_t n4 = static_cast<uint32_t>(n / 4);
+        if (n >= 16384u && n4 < 256u * 2048u) {
+            const uint32_t n1 = static_cast<uint32_t>(n);
+            hipLaunchKernelGGL((geglu_offset_vec_kernel<1>), dim3((n1 + 63) / 64), dim3(64), 0, stream, gate, ple,
+                               out, ple_offset, ple_row_stride, width, n1);
+            return hipGetLastError();
+        }
         const uint32_t threads = n4 >= 256u * 2048u ? 256u : 64u;
-        hipLaunchKernelGGL(geglu_offset_vec_kernel, dim3((n4 + threads - 1) / threads), dim3(threads), 0, stream,
-                           reinterpret_cast<const f32x4*>(gate), reinterpret_cast<const f32x4*>(ple),
-                           reinterpret_cast<f32x4*>(out), ple_offset / 4, ple_row_stride / 4, width / 4, n4);
+        hipLaunchKernelGGL((geglu_offset_vec_kernel<4>), dim3((n4 + threads - 1) / threads), dim3(threads), 0, stream,
+                           gate, ple, out, ple_offset / 4, ple_row_stride / 4, width / 4, n4);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(geglu_offset_kernel, dim3(grid_for(n)), dim3(256), 0, stream, gate, ple, out, ple_offset,

@@ -245,10 +245,11 @@ def test_geglu_offset_ple_slices(rt, ora):
 
 def test_geglu_offset_extremes_and_scalar_shapes(rt, ora):
     """Overflowing and infinite gates in some wavefronts (the guarded
-    GELU form) beside ordinary ones, on the 4-wide kernel (width 256) and on
-    the scalar one (width 37, offsets not divisible by 4)."""
+    GELU form) beside ordinary ones, on each vector form (width 256: one
+    value per lane from 16384 values, four per lane below that and from 2^21
+    values) and on the scalar one (width 37, offsets not divisible by 4)."""
     r = wl.rng(24)
-    for rows, layers, width, layer in [(96, 35, 256, 3), (50, 7, 37, 5)]:
+    for rows, layers, width, layer in [(96, 35, 256, 3), (40, 35, 256, 9), (8200, 2, 256, 1), (50, 7, 37, 5)]:
         gate = r.uniform(-30, 30, rows * width).astype(f32)
         gate[[3, 700, 701, rows * width * 3 // 4]] = [np.inf, -np.inf, f32(-3e13), f32(1e20)]
         gate[rows * width - 1] = f32(-1e20)
