@@ -251,8 +251,10 @@ __device__ __forceinline__ void sq_p(float* dst, const pvec<P>& x) {
 // region, so the handoff between the lanes that square and the lanes that
 // fold is a wavefront-scope fence, not a workgroup barrier.  SPLIT: a
 // token's units are spread over ceil(units / MAXU) consecutive wavefronts,
-// MAXU each (TPW = 1).
-template <int P, int MAXU, int TPW, int WPG, bool SPLIT = false>
+// MAXU each (TPW = 1).  SEQ = false (ATLAS_REDUCTION_WIDE): each unit's sum
+// of squares is a wavefront tree sum of the lanes' partial sums instead of
+// the in-order fold (no LDS), tolerance-level against the CPU operator.
+template <int P, int MAXU, int TPW, int WPG, bool SPLIT = false, bool SEQ = true>
 __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
     const float* q, const float* k, const float* q_weight, const float* k_weight, const float* cosine,
     const float* sine, float* q_out, float* k_out, uint32_t tokens, uint32_t q_heads, uint32_t has_key,
@@ -260,7 +262,7 @@ __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
     constexpr uint32_t HALF = 64 * P;
     constexpr uint32_t D = 2 * HALF;
     constexpr uint32_t STRIDE = D + 4;
-    __shared__ __align__(16) float sq_all[WPG][TPW * MAXU * STRIDE];
+    __shared__ __align__(16) float sq_all[WPG][SEQ ? TPW * MAXU * STRIDE : 4];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
     float* sq = sq_all[wave];
@@ -305,24 +307,43 @@ __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
     const float* kw = has_key ? k_weight : q_weight;
     const pvec<P> kwl = ld_p<P, false>(kw + p0), kwh = ld_p<P, false>(kw + HALF + p0);
 
-#pragma unroll
-    for (int i = 0; i < TPW; ++i)
-#pragma unroll
-        for (int u = 0; u < MAXU; ++u) {
-            sq_p<P>(sq + (i * MAXU + u) * STRIDE + p0, lo[i][u]);
-            sq_p<P>(sq + (i * MAXU + u) * STRIDE + HALF + p0, hi[i][u]);
-        }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // lane i * MAXU + u folds unit u of the wavefront's token i, in index order
+    // lane i * MAXU + u holds the sum of squares of unit u of the
+    // wavefront's token i
     float sum = 0.0f;
     const uint32_t li = lane / MAXU, lu = lane - li * MAXU;
     const bool folds = li < ntok && ubase + lu < total;
-    if (folds) {
-        const f32x4* row = reinterpret_cast<const f32x4*>(sq + lane * STRIDE);
+    if constexpr (SEQ) {
 #pragma unroll
-        for (uint32_t c = 0; c < D / 4; c += 64) sum = fold_lds_chunk(row + c, D / 4 - c < 64 ? D / 4 - c : 64, sum);
+        for (int i = 0; i < TPW; ++i)
+#pragma unroll
+            for (int u = 0; u < MAXU; ++u) {
+                sq_p<P>(sq + (i * MAXU + u) * STRIDE + p0, lo[i][u]);
+                sq_p<P>(sq + (i * MAXU + u) * STRIDE + HALF + p0, hi[i][u]);
+            }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // in index order
+        if (folds) {
+            const f32x4* row = reinterpret_cast<const f32x4*>(sq + lane * STRIDE);
+#pragma unroll
+            for (uint32_t c = 0; c < D / 4; c += 64)
+                sum = fold_lds_chunk(row + c, D / 4 - c < 64 ? D / 4 - c : 64, sum);
+        }
+    } else {
+        (void)sq;
+#pragma unroll
+        for (int i = 0; i < TPW; ++i)
+#pragma unroll
+            for (int u = 0; u < MAXU; ++u) {
+                float part = 0.0f;
+#pragma unroll
+                for (int j = 0; j < P; ++j) part = part + lo[i][u].v[j] * lo[i][u].v[j];
+#pragma unroll
+                for (int j = 0; j < P; ++j) part = part + hi[i][u].v[j] * hi[i][u].v[j];
+                const float t = wave_sum_tree_f32(part);
+                sum = lane == static_cast<uint32_t>(i * MAXU + u) ? t : sum;
+            }
     }
     const float inv = folds ? inverse_rms(sum, static_cast<float>(D), epsilon) : 0.0f;
 
@@ -356,7 +377,7 @@ __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
     }
 }
 
-template <int P, int TPW, int WPG>
+template <int P, int TPW, int WPG, bool SEQ>
 hipError_t launch_qk_token_cfg(hipStream_t s, const float* q, const float* k, const float* qw, const float* kw,
                                const float* c, const float* sn, float* qo, float* ko, uint32_t tokens,
                                uint32_t q_heads, uint32_t has_key, uint32_t rope_stride, float eps) {
@@ -365,8 +386,8 @@ hipError_t launch_qk_token_cfg(hipStream_t s, const float* q, const float* k, co
     const dim3 grid((waves + WPG - 1) / WPG);
 #define ATLAS_QK_CASE(U)                                                                                          \
     if (total <= U) {                                                                                             \
-        hipLaunchKernelGGL((qk_norm_rope_token_kernel<P, U, TPW, WPG>), grid, dim3(64 * WPG), 0, s, q, k, qw, kw, \
-                           c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);                           \
+        hipLaunchKernelGGL((qk_norm_rope_token_kernel<P, U, TPW, WPG, false, SEQ>), grid, dim3(64 * WPG), 0, s, q, \
+                           k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);                \
         return hipGetLastError();                                                                                 \
     }
     ATLAS_QK_CASE(1)
@@ -381,14 +402,14 @@ hipError_t launch_qk_token_cfg(hipStream_t s, const float* q, const float* k, co
 }
 
 // A token's units over ceil(units / U) wavefronts, one wavefront per workgroup.
-template <int P, int U>
+template <int P, int U, bool SEQ>
 hipError_t launch_qk_split(hipStream_t s, const float* q, const float* k, const float* qw, const float* kw,
                            const float* c, const float* sn, float* qo, float* ko, uint32_t tokens, uint32_t q_heads,
                            uint32_t has_key, uint32_t rope_stride, float eps) {
     const uint32_t total = q_heads + has_key;
     const uint64_t waves = static_cast<uint64_t>(tokens) * ((total + U - 1) / U);
     if (waves > 0x7fffffffu) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((qk_norm_rope_token_kernel<P, U, 1, 1, true>), dim3(static_cast<uint32_t>(waves)), dim3(64), 0,
+    hipLaunchKernelGGL((qk_norm_rope_token_kernel<P, U, 1, 1, true, SEQ>), dim3(static_cast<uint32_t>(waves)), dim3(64), 0,
                        s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
     return hipGetLastError();
 }
@@ -412,19 +433,19 @@ hipError_t launch_qk_split(hipStream_t s, const float* q, const float* k, const 
 // token; one token 2.55 (one unit), 2.69 (two), 3.97 (one wavefront); 16 and
 // 128 tokens favour one unit per wavefront (2.99 against 3.16, 3.46 against
 // 3.75), 32 and 64 tie.
-template <int P>
+template <int P, bool SEQ>
 hipError_t launch_qk_token_p(hipStream_t s, const float* q, const float* k, const float* qw, const float* kw,
                              const float* c, const float* sn, float* qo, float* ko, uint32_t tokens,
                              uint32_t q_heads, uint32_t has_key, uint32_t rope_stride, float eps) {
     if (tokens >= 2048)
-        return launch_qk_token_cfg<P, 1, 4>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride,
+        return launch_qk_token_cfg<P, 1, 4, SEQ>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride,
                                             eps);
     if (tokens >= 768)
-        return launch_qk_token_cfg<P, 1, 1>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride,
+        return launch_qk_token_cfg<P, 1, 1, SEQ>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride,
                                             eps);
     if (tokens >= 256)
-        return launch_qk_split<P, 2>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
-    return launch_qk_split<P, 1>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
+        return launch_qk_split<P, 2, SEQ>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
+    return launch_qk_split<P, 1, SEQ>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
 }
 
 // Generic head_dim fallback (even head_dim not of the form 64*V): one wave
@@ -637,23 +658,28 @@ hipError_t launch_qk_norm_rope_f32(hipStream_t stream, Reduction red, const floa
     // reorders the sum of squares here; kAuto keeps the sequential fold
     const bool seq = red != kWide;
     // Token engine: head_dim = 128*P, at most 16 units per token, operands
-    // and per-token cos/sin rows aligned to P floats.
+    // and per-token cos/sin rows aligned to P floats; the in-order fold, or
+    // under WIDE the wavefront tree sum.  Measured on MI355X (C5 decode, 8 Q
+    // heads + K, head_dim 256): WIDE took 12.7 us at 256 tokens and 9.5 at
+    // one token on the unit engine below, which puts 16 units on one
+    // wavefront one after another.
     {
         const uint32_t P = head_dim / 128;
         const uintptr_t pa = 4u * (P == 0 ? 1 : P) > 16 ? 16 : 4u * (P == 0 ? 1 : P);
-        const bool ok = seq && head_dim % 128 == 0 && (P == 1 || P == 2 || P == 4) && q_heads + has_key <= 16 &&
+        const bool ok = head_dim % 128 == 0 && (P == 1 || P == 2 || P == 4) && q_heads + has_key <= 16 &&
                         q_heads + has_key > 0 && aligned(q, pa) && aligned(q_out, pa) && aligned(q_weight, pa) &&
                         aligned(cosine, pa) && aligned(sine, pa) && rope_stride % P == 0 &&
                         (!has_key || (aligned(k, pa) && aligned(k_out, pa) && aligned(k_weight, pa)));
         if (ok) {
-            if (P == 1)
-                return launch_qk_token_p<1>(stream, q, k, q_weight, k_weight, cosine, sine, q_out, k_out, tokens,
-                                            q_heads, has_key, rope_stride, epsilon);
-            if (P == 2)
-                return launch_qk_token_p<2>(stream, q, k, q_weight, k_weight, cosine, sine, q_out, k_out, tokens,
-                                            q_heads, has_key, rope_stride, epsilon);
-            return launch_qk_token_p<4>(stream, q, k, q_weight, k_weight, cosine, sine, q_out, k_out, tokens,
-                                        q_heads, has_key, rope_stride, epsilon);
+#define ATLAS_QK_TOKEN(PP)                                                                                        \
+    return seq ? launch_qk_token_p<PP, true>(stream, q, k, q_weight, k_weight, cosine, sine, q_out, k_out, tokens, \
+                                             q_heads, has_key, rope_stride, epsilon)                                 \
+               : launch_qk_token_p<PP, false>(stream, q, k, q_weight, k_weight, cosine, sine, q_out, k_out,         \
+                                              tokens, q_heads, has_key, rope_stride, epsilon);
+            if (P == 1) ATLAS_QK_TOKEN(1)
+            if (P == 2) ATLAS_QK_TOKEN(2)
+            ATLAS_QK_TOKEN(4)
+#undef ATLAS_QK_TOKEN
         }
     }
     // Unit engine: head_dim = 64*V, 16-byte aligned operands (8-byte for V=2),

@@ -439,13 +439,17 @@ def test_wide_reduction_is_tolerance_level(rt, ora):
         exp_n, exp_o = cases.rms_oracle(ora, inp, m2)
         assert np.max(np.abs(got_n - exp_n) / np.abs(exp_n)) <= 1e-5
         assert np.linalg.norm(got_o - exp_o) / np.linalg.norm(exp_o) <= 1e-6
-        qinp, qm = cases.qk_case(64, 8, 256, 128, 1e4, 1e-6, 92)
-        tables = rope_tables_gemma4(qinp["pos"], 128, 256, 1e4)
-        say("wide qk")
-        gq = cases.qk_gpu(rt, qinp, qm, tables)
-        eq = cases.qk_oracle(ora, qinp, qm)
-        for g_, e_ in zip(gq, eq):
-            assert np.linalg.norm(g_ - e_) / np.linalg.norm(e_) <= 1e-6
+        # every token engine (one or two units per wavefront, one or four
+        # tokens per workgroup) at head_dim 256, and head_dim 128 and 512
+        for tokens, heads, d in [(64, 8, 256), (300, 8, 256), (1000, 8, 256), (2051, 8, 256), (37, 4, 128),
+                                 (300, 8, 512)]:
+            qinp, qm = cases.qk_case(tokens, heads, d, d // 2, 1e4, 1e-6, 92 + tokens)
+            tables = rope_tables_gemma4(qinp["pos"], d // 2, d, 1e4)
+            say(f"wide qk tokens={tokens} heads={heads} head_dim={d}")
+            gq = cases.qk_gpu(rt, qinp, qm, tables)
+            eq = cases.qk_oracle(ora, qinp, qm)
+            for g_, e_ in zip(gq, eq):
+                assert np.linalg.norm(g_ - e_) / np.linalg.norm(e_) <= 1e-6
     finally:
         rt.set_reduction(ATLAS_REDUCTION_SEQUENTIAL)
 
