@@ -324,9 +324,10 @@ template <int J, int MODE, bool PAIR, bool DEFER = false, int POL = -1>
 __global__ __launch_bounds__(256) void rms_tree_kernel(NormArgs a) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
-    const uint32_t r0 = blockIdx.x * 4 + wave;
+    const uint32_t wpb = blockDim.x >> 6;  // wavefronts per workgroup (1 or 4)
+    const uint32_t r0 = blockIdx.x * wpb + wave;
     if (r0 >= a.rows) return;  // wavefront-uniform
-    const uint32_t r1 = r0 + gridDim.x * 4;
+    const uint32_t r1 = r0 + gridDim.x * wpb;
     const bool second = PAIR && r1 < a.rows;
     const uint32_t nv = a.hidden >> 2;
     const float* operand = MODE == kNormAddScale ? a.out : a.residual;
@@ -687,6 +688,11 @@ hipError_t launch_reg(hipStream_t s, const NormArgs& a) {
 // fill the chip when each takes two).
 bool tree_pairs(uint32_t rows) { return rows >= 4096; }
 
+// Wavefronts (rows) per workgroup: one below 2048 rows, so a decode batch
+// spreads over every CU instead of a quarter of them (C5 epilogues at 256
+// rows under ATLAS_REDUCTION_WIDE: 3.37 against 3.60 us), four above.
+uint32_t tree_waves_per_group(uint32_t rows) { return rows < 2048 ? 1u : 4u; }
+
 // The residual and add-scale epilogues need their operand only after the
 // sum: it is requested after both rows' x (DEFER).  Measured on MI355X at
 // [4096, 1536] (residual, ATLAS_REDUCTION_WIDE): 12.98-13.03 us against
@@ -700,11 +706,12 @@ hipError_t launch_tree_j(hipStream_t s, const NormArgs& a) {
     constexpr int kStorePolicy = 2;
     const bool pair = tree_pairs(a.rows);
     const uint32_t waves = pair ? (a.rows + 1) / 2 : a.rows;
-    const dim3 grid((waves + 3) / 4);
+    const uint32_t wpb = tree_waves_per_group(a.rows);
+    const dim3 grid((waves + wpb - 1) / wpb);
     if (pair)
-        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, true, kDefer, kStorePolicy>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, true, kDefer, kStorePolicy>), grid, dim3(64 * wpb), 0, s, a);
     else
-        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, false, kDefer, kStorePolicy>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, false, kDefer, kStorePolicy>), grid, dim3(64 * wpb), 0, s, a);
     return hipGetLastError();
 }
 
@@ -1049,9 +1056,10 @@ __global__ __launch_bounds__(256) void rms_tree_f16_kernel(const uint16_t* x, co
                                                            float epsilon) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
-    const uint32_t r0 = blockIdx.x * 4 + wave;
+    const uint32_t wpb = blockDim.x >> 6;  // wavefronts per workgroup (1 or 4)
+    const uint32_t r0 = blockIdx.x * wpb + wave;
     if (r0 >= rows) return;  // wavefront-uniform
-    const uint32_t r1 = r0 + gridDim.x * 4;
+    const uint32_t r1 = r0 + gridDim.x * wpb;
     const bool second = PAIR && r1 < rows;
     const uint32_t n8 = hidden >> 3;
     TreeRowF16<J, ADD> row0, row1;
@@ -1185,12 +1193,13 @@ hipError_t launch_f16_tree_j(hipStream_t s, const uint16_t* x, const uint16_t* r
                              uint16_t* residual_out, uint16_t* out, uint32_t rows, uint32_t hidden, float eps) {
     const bool pair = tree_pairs(rows);
     const uint32_t waves = pair ? (rows + 1) / 2 : rows;
-    const dim3 grid((waves + 3) / 4);
+    const uint32_t wpb = tree_waves_per_group(rows);
+    const dim3 grid((waves + wpb - 1) / wpb);
     if (pair)
-        hipLaunchKernelGGL((rms_tree_f16_kernel<J, ADD, true>), grid, dim3(256), 0, s, x, residual, weight,
+        hipLaunchKernelGGL((rms_tree_f16_kernel<J, ADD, true>), grid, dim3(64 * wpb), 0, s, x, residual, weight,
                            residual_out, out, rows, hidden, eps);
     else
-        hipLaunchKernelGGL((rms_tree_f16_kernel<J, ADD, false>), grid, dim3(256), 0, s, x, residual, weight,
+        hipLaunchKernelGGL((rms_tree_f16_kernel<J, ADD, false>), grid, dim3(64 * wpb), 0, s, x, residual, weight,
                            residual_out, out, rows, hidden, eps);
     return hipGetLastError();
 }
