@@ -477,7 +477,9 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
     // the later chunks of a row land together, and the last one's in-order
     // adds would run after the read window closes.  Measured on MI355X at
     // [4096, 1536], residual: 13.68 against 13.98 us; the last two chunks
-    // 13.90, the last three 13.98, every chunk after the first 14.9.
+    // 13.90, the last three 13.98, every chunk after the first 14.9.  With
+    // the event lanes' folds done speculatively by every lane: one chunk
+    // 13.65-13.66, two 13.68-13.69, three 13.71-13.72.
     constexpr int kTailN = 1;
     constexpr bool kTail = !PAR && J > 1;
 #pragma unroll
