@@ -410,6 +410,62 @@ __device__ __forceinline__ uint32_t wave_inclusive_scan_u32(uint32_t v) {
     return v;
 }
 
+// One binade's scan of a chunk: each lane's ulps (0 for a lane that must
+// fold in f32: a tie, an out-of-range count, NaN or inf), their inclusive
+// wave prefix sum, and the mask of the f32 lanes.
+struct ChunkScan {
+    uint32_t inc, incl;
+    uint64_t bad;
+};
+
+template <int S>
+__device__ __forceinline__ ChunkScan chunk_scan(const float (&v)[S], uint32_t ex) {
+    const float inv_ulp = __uint_as_float((277u - ex) << 23);  // 2^(23-E)
+    float ulps = 0.0f, dev = 0.0f;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+        const float q = v[i] * inv_ulp;
+        const float m = __builtin_rintf(q);
+        dev = fmaxf(dev, __builtin_fabsf(q - m));
+        ulps = ulps + m;
+    }
+    const bool bad = !(ulps < 2097152.0f) || dev == 0.5f;  // out of range, NaN/inf, or a tie
+    ChunkScan c;
+    c.inc = bad ? 0u : static_cast<uint32_t>(ulps);
+    c.incl = wave_inclusive_scan_u32(c.inc);
+    c.bad = __builtin_amdgcn_ballot_w64(bad);
+    return c;
+}
+
+// The event loop in binade ex (sb's, within [27, 251]) from lane l0 with that
+// binade's scan: returns the lane to continue from (64 when the chunk is
+// done; otherwise the sum has left the binade and needs the next one's scan).
+template <int S>
+__device__ __forceinline__ uint32_t chunk_walk(const ChunkScan& c, const float (&v)[S], uint32_t& sb, uint32_t l0,
+                                               uint32_t ex) {
+    uint32_t base = l0 ? readlane_u32(c.incl, l0 - 1) : 0u;
+    for (;;) {
+        // every lane from its start as the event lane (lanes [l0, lc)
+        // stay in the binade, so lane lc's start is exact); issued ahead
+        // of the event search, which it does not depend on
+        float s = __uint_as_float(sb + (c.incl - c.inc) - base);
+#pragma unroll
+        for (int i = 0; i < S; ++i) s = s + v[i];
+        const uint32_t room = 0x800000u - (sb & 0x7fffffu);  // ulps to the next power of two
+        const uint64_t ev = (__builtin_amdgcn_ballot_w64(c.incl - base >= room) | c.bad) & (~0ull << l0);
+        __asm__ volatile("" ::"v"(s));  // keep the chain ahead of the branch
+        if (ev == 0) {
+            sb += readlane_u32(c.incl, 63) - base;
+            return 64;
+        }
+        const uint32_t lc = static_cast<uint32_t>(__builtin_ctzll(ev));
+        sb = readlane_u32(__float_as_uint(s), lc);
+        base = readlane_u32(c.incl, lc);
+        l0 = lc + 1;
+        if (l0 >= 64 || (sb >> 23) != ex) return l0;
+    }
+}
+
 // The same from lane `start` on (lanes before it are already folded).
 template <int S>
 __device__ __forceinline__ uint32_t fold_chunk_exact_from(const float (&v)[S], uint32_t sb, uint32_t start) {
@@ -424,41 +480,7 @@ __device__ __forceinline__ uint32_t fold_chunk_exact_from(const float (&v)[S], u
             ++l0;
             continue;
         }
-        const float inv_ulp = __uint_as_float((277u - ex) << 23);  // 2^(23-E)
-        float ulps = 0.0f, dev = 0.0f;
-#pragma unroll
-        for (int i = 0; i < S; ++i) {
-            const float q = v[i] * inv_ulp;
-            const float m = __builtin_rintf(q);
-            dev = fmaxf(dev, __builtin_fabsf(q - m));
-            ulps = ulps + m;
-        }
-        const bool bad = !(ulps < 2097152.0f) || dev == 0.5f;  // out of range, NaN/inf, or a tie
-        const uint32_t inc = bad ? 0u : static_cast<uint32_t>(ulps);
-        const uint32_t incl = wave_inclusive_scan_u32(inc);
-        const uint64_t badmask = __builtin_amdgcn_ballot_w64(bad);
-        uint32_t base = l0 ? readlane_u32(incl, l0 - 1) : 0u;
-        for (;;) {
-            // every lane from its start as the event lane (lanes [l0, lc)
-            // stay in the binade, so lane lc's start is exact); issued ahead
-            // of the event search, which it does not depend on
-            float s = __uint_as_float(sb + (incl - inc) - base);
-#pragma unroll
-            for (int i = 0; i < S; ++i) s = s + v[i];
-            const uint32_t room = 0x800000u - (sb & 0x7fffffu);  // ulps to the next power of two
-            const uint64_t ev = (__builtin_amdgcn_ballot_w64(incl - base >= room) | badmask) & (~0ull << l0);
-            __asm__ volatile("" ::"v"(s));  // keep the chain ahead of the branch
-            if (ev == 0) {
-                sb += readlane_u32(incl, 63) - base;
-                l0 = 64;
-                break;
-            }
-            const uint32_t lc = static_cast<uint32_t>(__builtin_ctzll(ev));
-            sb = readlane_u32(__float_as_uint(s), lc);
-            base = readlane_u32(incl, lc);
-            l0 = lc + 1;
-            if (l0 >= 64 || (sb >> 23) != ex) break;
-        }
+        l0 = chunk_walk<S>(chunk_scan<S>(v, ex), v, sb, l0, ex);
     }
     return sb;
 }
@@ -466,6 +488,26 @@ __device__ __forceinline__ uint32_t fold_chunk_exact_from(const float (&v)[S], u
 template <int S>
 __device__ __forceinline__ uint32_t fold_chunk_exact(const float (&v)[S], uint32_t sb) {
     return fold_chunk_exact_from<S>(v, sb, 0u);
+}
+
+// Two independent rows' chunks: both first scans are computed before either
+// event loop, so their VALU chains overlap; each row then takes the same
+// steps as fold_chunk_exact.
+template <int S>
+__device__ __forceinline__ void fold_chunk_exact_pair(const float (&v0)[S], uint32_t& sb0, const float (&v1)[S],
+                                                      uint32_t& sb1) {
+    const uint32_t ex0 = sb0 >> 23, ex1 = sb1 >> 23;
+    if (ex0 < 27 || ex0 > 251 || ex1 < 27 || ex1 > 251) {
+        sb0 = fold_chunk_exact_from<S>(v0, sb0, 0u);
+        sb1 = fold_chunk_exact_from<S>(v1, sb1, 0u);
+        return;
+    }
+    const ChunkScan c0 = chunk_scan<S>(v0, ex0);
+    const ChunkScan c1 = chunk_scan<S>(v1, ex1);
+    const uint32_t l0 = chunk_walk<S>(c0, v0, sb0, 0u, ex0);
+    const uint32_t l1 = chunk_walk<S>(c1, v1, sb1, 0u, ex1);
+    if (l0 < 64) sb0 = fold_chunk_exact_from<S>(v0, sb0, l0);
+    if (l1 < 64) sb1 = fold_chunk_exact_from<S>(v1, sb1, l1);
 }
 
 // ---------------------------------------------------------------------------

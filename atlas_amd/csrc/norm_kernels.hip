@@ -487,6 +487,7 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
         const uint32_t creal = lane + 64u * j;
         const uint32_t c = min(creal, nv - 1);
         const bool par_chunk = PAR ? j > 0 : (kTail && j >= J - kTailN);
+        float sqr[R][4];  // a wave-parallel chunk's squares, row by row
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             f32x4 v = x[r][j];
@@ -502,13 +503,27 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
                 // width: adding +0 leaves a sum of squares unchanged)
                 sq4[r * stride4 + creal] = creal < nv ? f32x4{v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w}
                                                       : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            } else if (static_cast<uint32_t>(r) < nrows) {
+            } else {
                 // chunks after the first: exact wave-parallel fold (columns past
                 // the row width hold clamped duplicates and contribute +0)
                 const bool in_row = creal < nv;
-                const float sq[4] = {in_row ? v.x * v.x : 0.0f, in_row ? v.y * v.y : 0.0f,
-                                     in_row ? v.z * v.z : 0.0f, in_row ? v.w * v.w : 0.0f};
-                sb[r] = fold_chunk_exact<4>(sq, sb[r]);
+                sqr[r][0] = in_row ? v.x * v.x : 0.0f;
+                sqr[r][1] = in_row ? v.y * v.y : 0.0f;
+                sqr[r][2] = in_row ? v.z * v.z : 0.0f;
+                sqr[r][3] = in_row ? v.w * v.w : 0.0f;
+            }
+        }
+        if (par_chunk && !kRun) {
+            // two rows' scans side by side, else row by row (measured on
+            // MI355X, residual at [4096, 1536]: 13.50-13.52 against
+            // 13.63-13.65 us row by row; the inverse RMS likewise one chain
+            // for both rows, below)
+            if (R == 2 && nrows == 2) {
+                fold_chunk_exact_pair<4>(sqr[0], sb[0], sqr[R - 1], sb[R - 1]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+                    if (static_cast<uint32_t>(r) < nrows) sb[r] = fold_chunk_exact<4>(sqr[r], sb[r]);
             }
         }
         if (!par_chunk && !kRun) {
@@ -560,13 +575,28 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
         }
     }
 
-    const float inv = lane < nrows ? inverse_rms(s, static_cast<float>(h), a.epsilon) : 0.0f;
+    // lane r < nrows: row r's inverse RMS, one chain for every row (the
+    // wave-parallel fold leaves row r's sum in sb[r], the in-order one in
+    // lane r's s).  A single row with the wave-parallel fold computes it
+    // uniformly instead, without the readlane.  Measured on MI355X: the
+    // residual epilogue at [4096, 1536] (two rows) 13.61-13.62 against
+    // 13.67-13.79 us with a chain per row; C5 at 256 rows (one) 4.74-4.79
+    // against 4.70-4.73 with the readlane.
+    constexpr bool kUniform = (PAR || kTail) && R == 1;
+    float sum_r = s;
+    if constexpr (PAR || kTail) {
+        uint32_t mine = sb[0];
+#pragma unroll
+        for (int r = 1; r < R; ++r) mine = lane == static_cast<uint32_t>(r) ? sb[r] : mine;
+        sum_r = __uint_as_float(mine);
+    }
+    const float inv = lane < nrows ? inverse_rms(sum_r, static_cast<float>(h), a.epsilon) : 0.0f;
     const float scale = MODE == kNormAddScale ? *a.scale : 1.0f;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         if (static_cast<uint32_t>(r) >= nrows) break;
-        const float ir = (PAR || kTail) ? inverse_rms(__uint_as_float(sb[r]), static_cast<float>(h), a.epsilon)
-                             : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
+        const float ir = kUniform ? inverse_rms(__uint_as_float(sb[0]), static_cast<float>(h), a.epsilon)
+                                  : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), r));
         const size_t base = static_cast<size_t>(row0 + r) * h;
         f32x4 n[J];
         auto emit = [&](int j) {
