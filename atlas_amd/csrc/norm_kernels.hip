@@ -472,15 +472,17 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
 
     float s = 0.0f;  // lane r < nrows: running sum of squares of row r
     uint32_t sb[R];  // PAR: running sums of squares (bit patterns, wave-uniform)
-    // In-order engine (!PAR): the row's last chunk takes the exact
-    // wave-parallel fold instead (one per row, after the in-order chunks):
-    // the later chunks of a row land together, and the last one's in-order
-    // adds would run after the read window closes.  Measured on MI355X at
-    // [4096, 1536], residual: 13.68 against 13.98 us; the last two chunks
-    // 13.90, the last three 13.98, every chunk after the first 14.9.  With
-    // the event lanes' folds done speculatively by every lane: one chunk
-    // 13.65-13.66, two 13.68-13.69, three 13.71-13.72.
-    constexpr int kTailN = 1;
+    // In-order engine (!PAR): the row's last two chunks take the exact
+    // wave-parallel fold instead (after the in-order chunks): the later
+    // chunks of a row land together, and their in-order adds would run
+    // after the read window closes.  Measured on MI355X at [4096, 1536],
+    // residual, with both rows' scans side by side: the last two chunks
+    // 13.40-13.55 us (mean 13.46 over six runs on two boxes), the last one
+    // 13.45-13.56 (13.49), the last three 13.44-13.52 (13.48); with the
+    // rows one after the other and the event lanes' values broadcast from
+    // LDS, the last chunk 13.68 against 13.98 in order, the last two 13.90,
+    // the last three 13.98, every chunk after the first 14.9.
+    constexpr int kTailN = 2;
     constexpr bool kTail = !PAR && J > 1;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
