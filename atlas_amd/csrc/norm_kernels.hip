@@ -482,8 +482,10 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
     // rows one after the other and the event lanes' values broadcast from
     // LDS, the last chunk 13.68 against 13.98 in order, the last two 13.90,
     // the last three 13.98, every chunk after the first 14.9.
-    constexpr int kTailN = 2;
+    // (chunk 0 always folds in order: it sets the sum the tail continues)
+    constexpr int kTailN = J > 2 ? 2 : 1;
     constexpr bool kTail = !PAR && J > 1;
+    static_assert(!kTail || kTailN < J, "the in-order head must precede the parallel tail");
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const uint32_t creal = lane + 64u * j;
