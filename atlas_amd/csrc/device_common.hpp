@@ -511,6 +511,82 @@ __device__ __forceinline__ void fold_chunk_exact_pair(const float (&v0)[S], uint
 }
 
 // ---------------------------------------------------------------------------
+// The in-order fold of a row's first 256 squares, with its chain cut by four.
+//
+// The head is four segments of 64.  Segment 0 starts at exactly 0; segment
+// k's start is the fold of the segments before it, known only once they are
+// folded -- but approximately known at once: a wave prefix sum of the lanes'
+// partial sums estimates it within a few ulps (the in-order fold and the
+// estimate differ by their rounding errors, a few ulps over <= 192 adds).  So
+// 21 lanes per segment fold it in parallel from 21 consecutive floats around
+// the estimate, and the segments are chained by selection: segment k's exact
+// start (the selected fold of segment k - 1) picks the lane that started
+// there, whose result is bit for bit the in-order fold from that start.  A
+// start outside the window (a miss) folds that segment in order from it.
+// Every step is either the in-order fold's own f32 adds or a selection of
+// them, so the result is the in-order fold's bit pattern in every case.
+// Misses measured on MI355X: 12 in 107,776 Gaussian rows of 1536.
+//
+// h: the 64 float4 of squares in LDS, float4 i at h[i + i / 16] (a pad per
+// segment keeps the four segments' reads on distinct banks).  The whole
+// wavefront takes part; the result is wave-uniform.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_inclusive_scan_f32(float v) {  // any order: an estimate
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x111, 0xf, 0xf, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x112, 0xf, 0xf, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xf, 0xf, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xf, 0xf, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, false));
+    return v;
+}
+
+// 16 float4 folded in order from s (both groups of 8 read ahead of the adds)
+__device__ __forceinline__ float fold_lds_16(const f32x4* p, float s) {
+    f32x4 a[8], b[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = p[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b[i] = p[8 + i];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        s = s + a[i].x;
+        s = s + a[i].y;
+        s = s + a[i].z;
+        s = s + a[i].w;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        s = s + b[i].x;
+        s = s + b[i].y;
+        s = s + b[i].z;
+        s = s + b[i].w;
+    }
+    return s;
+}
+
+__device__ __forceinline__ float head_fold_candidates(const f32x4* h, uint32_t lane) {
+    const f32x4 mine = h[lane + lane / 16];
+    const float pre = wave_inclusive_scan_f32((mine.x + mine.y) + (mine.z + mine.w));
+    // lane 0: segment 0 from 0; lanes 1-21, 22-42, 43-63: segments 1-3
+    const uint32_t seg = lane == 0 ? 0u : (lane - 1) / 21 + 1;
+    const uint32_t j = lane == 0 ? 0u : (lane - 1) % 21;
+    const float e1 = readlane_f32(pre, 15), e2 = readlane_f32(pre, 31), e3 = readlane_f32(pre, 47);
+    const float est = seg == 1 ? e1 : (seg == 2 ? e2 : e3);
+    const uint32_t start = seg == 0 ? 0u : __float_as_uint(est) + j - 10u;  // est - 10 .. est + 10 ulps
+    const float res = fold_lds_16(h + 17 * seg, __uint_as_float(start));
+    float s = readlane_f32(res, 0);
+#pragma unroll
+    for (uint32_t k = 1; k < 4; ++k) {
+        const uint64_t m = __builtin_amdgcn_ballot_w64(seg == k && start == __float_as_uint(s));
+        s = m ? readlane_f32(res, static_cast<uint32_t>(__builtin_ctzll(m))) : fold_lds_16(h + 17 * k, s);
+    }
+    return s;
+}
+
+// ---------------------------------------------------------------------------
 // The continuation with its scans computed ahead.
 //
 // A sum of squares only grows, so its binade only moves up.  fold_scan_ahead

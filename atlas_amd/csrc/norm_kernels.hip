@@ -380,17 +380,23 @@ struct FoldScansLds {
     uint32_t e0;
 };
 
+// RUN: helper wavefronts, one binade's scans each.  Measured on MI355X (C5
+// epilogues, with the head folded by candidate segments): four helpers
+// 4.54-4.56 us at 256 rows and 3.28-3.39 at one row, against 4.61-4.65 and
+// 3.37-3.50 with two helpers of two binades each.
+constexpr int kRunHelpers = 4;
+
 template <int R, int J, int MODE, bool PAR, bool STAGE, bool RUN>
-__global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
+__global__ __launch_bounds__(RUN ? 64 * (kRunHelpers + 1) : 64) void rms_reg_kernel(NormArgs a) {
     // Squares of R rows, (hidden/4 + 1) float4 per row.  The load phase is
     // straight-line code (rows past the end and columns past the row width
     // are clamped to valid duplicate addresses and never stored), so the
     // compiler can wait for chunk j's loads alone before folding it.
     extern __shared__ f32x4 sq4[];
     constexpr bool kOperand = MODE != kNormPlain;
-    // RUN: one row; two more wavefronts compute the continuation's scans
-    // (fold_scan_ahead, two binades each) while the first folds the
-    // in-order head
+    // RUN: one row; kRunHelpers more wavefronts compute the continuation's
+    // scans (fold_scan_ahead, one binade each) while the first folds the
+    // head (head_fold_candidates)
     constexpr bool kRun = RUN && PAR && J > 1 && R == 1;
     constexpr int kRunS = 4 * (J > 1 ? J - 1 : 1);
     const uint32_t lane = threadIdx.x & 63u;
@@ -404,6 +410,8 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
     // second operand: residual (kNormResidual, kNormAddNorm) or state (kNormAddScale)
     const float* operand = MODE == kNormAddScale ? a.out : a.residual;
     FoldScansLds<4>* scans_lds = reinterpret_cast<FoldScansLds<4>*>(sq4 + stride4);
+    // RUN: chunk 0's squares again, laid out for head_fold_candidates
+    f32x4* head_pad = sq4 + stride4 + (sizeof(FoldScansLds<4>) + 15) / 16;
     // lane l's run: the 4 * (J - 1) consecutive squares from float4 64 + (J - 1) * l
     auto read_run = [&](float (&run)[kRunS]) {
 #pragma unroll
@@ -416,8 +424,9 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
         }
     };
     if constexpr (kRun) {
-        if (threadIdx.x >= 64) {  // the two helper wavefronts, two binades each
-            const uint32_t b0 = 2u * (static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) - 1u);
+        if (threadIdx.x >= 64) {  // the helper wavefronts
+            constexpr int kBph = 4 / kRunHelpers;
+            const uint32_t b0 = kBph * (static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) - 1u);
             __syncthreads();  // every square staged
             const f32x4 h0 = sq4[lane];
             const float approx = wave_sum_any_order_f32((h0.x + h0.y) + (h0.z + h0.w));
@@ -426,15 +435,15 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
             const uint32_t e0 = __float_as_uint(approx * 0.999f) >> 23;
             float run[kRunS];
             read_run(run);
-            const FoldScans<2> f = fold_scan_ahead<kRunS, 2>(run, e0 + b0);
+            const FoldScans<kBph> f = fold_scan_ahead<kRunS, kBph>(run, e0 + b0);
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
+            for (int b = 0; b < kBph; ++b) {
                 scans_lds->inc[b0 + b][lane] = f.inc[b];
                 scans_lds->incl[b0 + b][lane] = f.incl[b];
             }
             if (lane == 0) {
 #pragma unroll
-                for (int b = 0; b < 2; ++b) scans_lds->bad[b0 + b] = f.bad[b];
+                for (int b = 0; b < kBph; ++b) scans_lds->bad[b0 + b] = f.bad[b];
                 if (b0 == 0) scans_lds->e0 = e0;
             }
             __syncthreads();  // scans published
@@ -502,6 +511,7 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
             }
             if (!par_chunk) {
                 sq4[r * stride4 + c] = f32x4{v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w};
+                if (kRun && j == 0) head_pad[lane + lane / 16] = f32x4{v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w};
             } else if (kRun) {
                 // staged for the one-step continuation below (+0 past the row
                 // width: adding +0 leaves a sum of squares unchanged)
@@ -544,12 +554,14 @@ __global__ __launch_bounds__(RUN ? 192 : 64) void rms_reg_kernel(NormArgs a) {
     }
     if constexpr (kRun) {
         // The continuation (columns 256 .. 256 * J) as one run.  The helper
-        // wavefront computes its scans for four binades from a lower bound
-        // of the head's exponent while this one folds the head in order;
+        // wavefronts compute its scans for four binades from a lower bound
+        // of the head's exponent while this one folds the head (four
+        // segments folded from candidate starts and chained by selection,
+        // 5.13 -> 4.61 us per C5 epilogue at 256 rows with two helpers);
         // the walk then has only the fold's real events (binade crossings,
         // ties) left.
         __syncthreads();  // every square staged
-        const float head = fold_lds_chunk(sq4, 64u, 0.0f);
+        const float head = head_fold_candidates(head_pad, lane);
         __syncthreads();  // the helper's scans published
         FoldScans<4> f;
 #pragma unroll
@@ -664,9 +676,9 @@ RegConfig pick_reg(uint32_t rows, int mode) {
 // wavefronts (RUN).  Measured on MI355X: decode batches gain (C5 step at 256
 // rows: 29.5 -> 28.5 us per layer with one helper computing four binades,
 // 27.8 -> 26.8 with two helpers of two binades each, whose scans then land
-// before the head's in-order fold ends); from 2048 rows up the extra
-// wavefronts per row cost more than they hide ([4096, 1536]: 10.3 -> 13.9 us
-// with one helper).
+// before the head's in-order fold ends; kRunHelpers has the current count);
+// from 2048 rows up the extra wavefronts per row cost more than they hide
+// ([4096, 1536]: 10.3 -> 13.9 us with one helper).
 bool norm_run(uint32_t rows) { return rows < 2048; }
 
 template <int R, int J, int MODE>
@@ -677,12 +689,13 @@ hipError_t launch_reg_rj(hipStream_t s, const NormArgs& a, bool par) {
     // (30.2 -> 30.8 us per C5 layer).
     const bool stage = a.rows >= 2048;
     const bool run = par && J > 1 && R == 1 && norm_run(a.rows);
-    const size_t lds = run ? (64u * J + 1) * sizeof(f32x4) + sizeof(FoldScansLds<4>)
+    const size_t lds = run ? (64u * J + 1 + (sizeof(FoldScansLds<4>) + 15) / 16 + 68) * sizeof(f32x4)
                            : static_cast<size_t>(R) * (a.hidden / 4 + 1) * sizeof(f32x4);
     const dim3 grid((a.rows + R - 1) / R);
     if constexpr (R == 1 && J > 1) {
         if (run) {
-            hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, true>), grid, dim3(3 * kWave), lds, s, a);
+            hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, true>), grid, dim3((kRunHelpers + 1) * kWave),
+                               lds, s, a);
             return hipGetLastError();
         }
     }
