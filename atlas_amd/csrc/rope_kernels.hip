@@ -262,7 +262,12 @@ __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
     constexpr uint32_t HALF = 64 * P;
     constexpr uint32_t D = 2 * HALF;
     constexpr uint32_t STRIDE = D + 4;
-    __shared__ __align__(16) float sq_all[WPG][SEQ ? TPW * MAXU * STRIDE : 4];
+    // head_dim 256 with one unit per wavefront: the unit's sum by candidate
+    // segments (head_fold_candidates), from a padded copy of its squares
+    // (float f at f + 4 (f / 64), 68 float4)
+    constexpr bool kCand = SEQ && D == 256 && TPW == 1 && MAXU == 1;
+    constexpr uint32_t kLds = kCand ? 272 : (SEQ ? TPW * MAXU * STRIDE : 4);
+    __shared__ __align__(16) float sq_all[WPG][kLds];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
     float* sq = sq_all[wave];
@@ -312,7 +317,17 @@ __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
     float sum = 0.0f;
     const uint32_t li = lane / MAXU, lu = lane - li * MAXU;
     const bool folds = li < ntok && ubase + lu < total;
-    if constexpr (SEQ) {
+    if constexpr (kCand) {
+        // lane l's values p0, p0 + 1 (P = 2) and HALF + p0, ...: each pair
+        // inside one 64-float segment
+        sq_p<P>(sq + p0 + 4 * (p0 / 64), lo[0][0]);
+        sq_p<P>(sq + HALF + p0 + 4 * ((HALF + p0) / 64), hi[0][0]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const float t = head_fold_candidates(reinterpret_cast<const f32x4*>(sq), lane);
+        sum = lane == 0 ? t : sum;
+    } else if constexpr (SEQ) {
 #pragma unroll
         for (int i = 0; i < TPW; ++i)
 #pragma unroll
@@ -427,12 +442,13 @@ hipError_t launch_qk_split(hipStream_t s, const float* q, const float* k, const 
 //   1536        10.63        9.70      7.16          7.45
 //   2047        13.00       11.07      7.88          8.00
 // and at 4096 tokens 14.17 us with four wavefronts per workgroup against
-// 14.25-14.33 with one and 18.3 with two units per wavefront.  In the C5
-// decode step (a graph of 35 launches): 256 tokens 3.86 us with two units
-// per wavefront against 4.06-4.64 with one and 4.72 with one wavefront per
-// token; one token 2.55 (one unit), 2.69 (two), 3.97 (one wavefront); 16 and
-// 128 tokens favour one unit per wavefront (2.99 against 3.16, 3.46 against
-// 3.75), 32 and 64 tie.
+// 14.25-14.33 with one and 18.3 with two units per wavefront.  With one unit
+// per wavefront the unit's fold runs by candidate segments (head_dim 256),
+// which moves the first crossover: 256 tokens 3.87 against 4.08 us with two
+// units per wavefront, 384 4.31 against 4.39, 512 4.85 against 4.76, 767
+// 6.47 against 5.93.  In the C5 decode step (a graph of 35 launches): 256
+// tokens 3.59-3.60 us (3.86 with two units per wavefront, 4.72 with one
+// wavefront per token); one token 2.20-2.22 (2.55 with the in-order fold).
 template <int P, bool SEQ>
 hipError_t launch_qk_token_p(hipStream_t s, const float* q, const float* k, const float* qw, const float* kw,
                              const float* c, const float* sn, float* qo, float* ko, uint32_t tokens,
@@ -443,7 +459,7 @@ hipError_t launch_qk_token_p(hipStream_t s, const float* q, const float* k, cons
     if (tokens >= 768)
         return launch_qk_token_cfg<P, 1, 1, SEQ>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride,
                                             eps);
-    if (tokens >= 256)
+    if (tokens >= 512)
         return launch_qk_split<P, 2, SEQ>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
     return launch_qk_split<P, 1, SEQ>(s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
 }

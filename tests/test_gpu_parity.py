@@ -170,10 +170,11 @@ def test_reference_fusion_parity_seeds(rt, ora):
 @pytest.mark.parametrize("head_dim,rope_stride,q_heads,has_key", [
     (256, 128, 8, True), (256, 256, 8, True), (512, 256, 8, True), (128, 64, 4, True), (256, 128, 8, False),
     (96, 48, 3, True), (64, 32, 2, True)])
-@pytest.mark.parametrize("tokens", [37, 300, 1000, 2051])
+@pytest.mark.parametrize("tokens", [37, 300, 600, 1000, 2051])
 def test_qk_norm_rope_shapes(rt, ora, head_dim, rope_stride, q_heads, has_key, tokens):
-    """Each token engine: a token's units one per wavefront (37 tokens) or two
-    per wavefront (300; odd unit counts leave a last wavefront one unit), one
+    """Each token engine: a token's units one per wavefront (37 and 300
+    tokens; at head_dim 256 each unit folded by candidate segments) or two per
+    wavefront (600; odd unit counts leave a last wavefront one unit), one
     token per wavefront (1000) and four per workgroup (2051 tokens: a ragged
     last workgroup)."""
     inp, m = cases.qk_case(tokens, q_heads, head_dim, rope_stride, 1e6, 1e-6, 500 + head_dim, has_key, start=1000)
@@ -441,8 +442,8 @@ def test_wide_reduction_is_tolerance_level(rt, ora):
         assert np.linalg.norm(got_o - exp_o) / np.linalg.norm(exp_o) <= 1e-6
         # every token engine (one or two units per wavefront, one or four
         # tokens per workgroup) at head_dim 256, and head_dim 128 and 512
-        for tokens, heads, d in [(64, 8, 256), (300, 8, 256), (1000, 8, 256), (2051, 8, 256), (37, 4, 128),
-                                 (300, 8, 512)]:
+        for tokens, heads, d in [(64, 8, 256), (300, 8, 256), (600, 8, 256), (1000, 8, 256), (2051, 8, 256),
+                                 (37, 4, 128), (300, 8, 512)]:
             qinp, qm = cases.qk_case(tokens, heads, d, d // 2, 1e4, 1e-6, 92 + tokens)
             tables = rope_tables_gemma4(qinp["pos"], d // 2, d, 1e4)
             say(f"wide qk tokens={tokens} heads={heads} head_dim={d}")
