@@ -481,18 +481,18 @@ __global__ __launch_bounds__(RUN ? 64 * (kRunHelpers + 1) : 64) void rms_reg_ker
 
     float s = 0.0f;  // lane r < nrows: running sum of squares of row r
     uint32_t sb[R];  // PAR: running sums of squares (bit patterns, wave-uniform)
-    // In-order engine (!PAR): the row's last two chunks take the exact
+    // In-order engine (!PAR): the row's last three chunks take the exact
     // wave-parallel fold instead (after the in-order chunks): the later
     // chunks of a row land together, and their in-order adds would run
     // after the read window closes.  Measured on MI355X at [4096, 1536],
-    // residual, with both rows' scans side by side: the last two chunks
-    // 13.40-13.55 us (mean 13.46 over six runs on two boxes), the last one
-    // 13.45-13.56 (13.49), the last three 13.44-13.52 (13.48); with the
-    // rows one after the other and the event lanes' values broadcast from
-    // LDS, the last chunk 13.68 against 13.98 in order, the last two 13.90,
-    // the last three 13.98, every chunk after the first 14.9.
+    // residual, with both rows' scans side by side (means over three runs
+    // per box, two boxes): the last three chunks 13.41 and 13.48 us, the
+    // last two 13.46 and 13.50, the last one 13.49, every chunk after the
+    // first 14.03; with the rows one after the other and the event lanes'
+    // values broadcast from LDS, the last chunk 13.68 against 13.98 in
+    // order, the last two 13.90, the last three 13.98.
     // (chunk 0 always folds in order: it sets the sum the tail continues)
-    constexpr int kTailN = J > 2 ? 2 : 1;
+    constexpr int kTailN = J > 3 ? 3 : J - 1;
     constexpr bool kTail = !PAR && J > 1;
     static_assert(!kTail || kTailN < J, "the in-order head must precede the parallel tail");
 #pragma unroll
