@@ -183,6 +183,23 @@ def test_qk_norm_rope_shapes(rt, ora, head_dim, rope_stride, q_heads, has_key, t
     assert_bits("qk", cases.qk_gpu(rt, inp, m, tables), cases.qk_oracle(ora, inp, m))
 
 
+@pytest.mark.parametrize("tokens", [37, 300, 600, 1000])
+@pytest.mark.parametrize("head_dim", [256, 128])
+def test_qk_norm_rope_exact_fold_adversarial_heads(rt, ora, tokens, head_dim):
+    """Heads built to break a reordered or speculative fold (ties, binade
+    crossings, zeros, subnormal and overflowing squares, inf and NaN) through
+    each token engine: one unit per wavefront (37, 300; at head_dim 256 the
+    unit folded by candidate segments, whose misses take the in-order path),
+    two units per wavefront (600) and one token per wavefront (1000)."""
+    qh = 8
+    inp, m = cases.qk_case(tokens, qh, head_dim, head_dim // 2, 1e6, 1e-6, 700 + tokens + head_dim)
+    inp["q"] = cases.adversarial_rows(tokens * qh, head_dim, 800 + tokens).reshape(-1)
+    inp["k"] = cases.adversarial_rows(tokens, head_dim, 900 + tokens).reshape(-1)
+    tables = rope_tables_gemma4(inp["pos"], head_dim // 2, head_dim, 1e6)
+    say(f"qk_norm_rope adversarial tokens={tokens} head_dim={head_dim}")
+    assert_bits_nan_equal("qk", cases.qk_gpu(rt, inp, m, tables), cases.qk_oracle(ora, inp, m))
+
+
 def test_qk_norm_rope_in_place_and_decode_positions(rt, ora):
     d, qh, tokens = 256, 8, 256
     r = wl.rng(9)
