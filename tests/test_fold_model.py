@@ -26,6 +26,11 @@ reproduce the sequential f32 fold bit for bit on Gaussian rows, FP16-valued
 rows and the adversarial rows of the GPU tests (ties, binade crossings,
 zeros, subnormal and overflowing squares, inf, NaN, constant and geometric
 rows).  Planted mistakes (ignoring ties, ignoring binade crossings) must fail.
+
+The decode engines fold the first 256 squares by candidate segments
+(head_fold_candidates); its model at the end of this file is checked the same
+way, with windows narrow enough to force the in-order fallback, and with a
+planted mistake (the nearest candidate taken instead of the exact one).
 """
 import numpy as np
 import pytest
@@ -141,3 +146,78 @@ def test_planted_mistakes_fail():
             wrong = sum(_bits(sequential_fold(sq)) != _bits(exact_fold_model(sq, 4, **kw))
                         for sq in sq_rows if np.isfinite(sequential_fold(sq)))
             assert wrong > 0, kw
+
+
+# ---------------------------------------------------------------------------
+# The head by candidate segments (head_fold_candidates in device_common.hpp):
+# the first 256 squares as four segments of 64; segment 0 folds from 0,
+# segment k from the 2 * window + 1 consecutive floats around an estimate of
+# its start, and the exact start of segment k (the selected fold of segment
+# k - 1) selects the candidate that started there, or folds the segment in
+# order from it when none did (a miss).
+# ---------------------------------------------------------------------------
+def _fold_from(starts, vals):
+    """In-order f32 fold of vals from every start at once."""
+    s = np.asarray(starts, f32).copy()
+    for a in vals:
+        s = (s + a).astype(f32)
+    return s
+
+
+def candidate_head_model(sq256, window=10, exact=True):
+    seg = sq256.reshape(4, 64)
+    lanes = sq256.reshape(64, 4)
+    part = ((lanes[:, 0] + lanes[:, 1]) + (lanes[:, 2] + lanes[:, 3])).astype(f32)
+    pre = np.cumsum(part, dtype=f32)  # an estimate: any order would do
+    s = _fold_from([0.0], seg[0])[0]
+    misses = 0
+    for k in range(1, 4):
+        est = _bits(pre[16 * k - 1])
+        starts = (np.arange(est - window, est + window + 1, dtype=np.int64) & 0xFFFFFFFF).astype(u32)
+        res = _fold_from(starts.view(f32), seg[k])
+        want = _bits(s)
+        hit = np.nonzero(starts == want)[0]
+        if exact:
+            if hit.size:
+                s = res[hit[0]]
+            else:
+                s = _fold_from([s], seg[k])[0]
+                misses += 1
+        else:  # planted mistake: the nearest candidate, exact or not
+            s = res[int(np.argmin(np.abs(starts.astype(np.int64) - want)))]
+    return s, misses
+
+
+def _heads():
+    for name, x in _rows():
+        for row in x:
+            if row.size >= 256:
+                yield name, (row[:256] * row[:256]).astype(f32)
+
+
+@pytest.mark.parametrize("window", [10, 5, 1])
+def test_candidate_head_reproduces_the_sequential_fold(window):
+    checked = misses = 0
+    with np.errstate(over="ignore", invalid="ignore"):
+        for name, sq in _heads():
+            want = sequential_fold(sq)
+            got, m = candidate_head_model(sq, window)
+            assert _bits(want) == _bits(got) or (np.isnan(want) and np.isnan(got)), (name, window, want, got)
+            checked += 1
+            misses += m
+    assert checked > 1000
+    if window == 1:
+        assert misses > 0  # the in-order fallback was exercised
+
+
+def test_candidate_head_planted_mistake_fails():
+    """Taking the nearest candidate instead of the exact start's gives wrong bits."""
+    wrong = 0
+    with np.errstate(over="ignore", invalid="ignore"):
+        for name, sq in _heads():
+            want = sequential_fold(sq)
+            if not np.isfinite(want):
+                continue
+            got, _ = candidate_head_model(sq, 1, exact=False)
+            wrong += _bits(want) != _bits(got)
+    assert wrong > 0
