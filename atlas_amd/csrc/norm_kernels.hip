@@ -57,8 +57,29 @@ __device__ __forceinline__ float epilogue(const NormArgs& a, size_t idx, float x
     return (a.out[idx] + n) * scale;
 }
 
+// Kernel parameters of the NormArgs engines.  A by-value struct is not
+// preloaded into SGPRs, so the fields are passed one by one, in this order:
+// the counts and the pointers the first loads need (and epsilon) fill the
+// first 56 bytes, which arrive in user SGPRs at wave launch (kernarg
+// preload), so a wavefront's first row load waits on no scalar load; the
+// outputs written only at the end follow.  wpb (wavefronts per workgroup)
+// and pair_stride (the row distance of a wavefront's second row) come from
+// the host instead of blockDim / gridDim, which are kernarg loads too.
+#define ATLAS_NORM_KPARAMS                                                                               \
+    uint32_t p_rows, uint32_t p_hidden, uint32_t wpb, uint32_t pair_stride, const float* p_x,              \
+        const float* p_residual, const float* p_weight, float* p_out, float p_epsilon, float* p_normalized, \
+        float* p_residual_out, const float* p_scale
+#define ATLAS_NORM_UNPACK                                                                                  \
+    const NormArgs a {                                                                                     \
+        p_x, p_weight, p_residual, p_normalized, p_residual_out, p_out, p_scale, p_rows, p_hidden, p_epsilon \
+    }
+#define ATLAS_NORM_KARGS(a, wpb, pair_stride)                                                                   \
+    (a).rows, (a).hidden, (wpb), (pair_stride), (a).x, (a).residual, (a).weight, (a).out, (a).epsilon,          \
+        (a).normalized, (a).residual_out, (a).scale
+
 template <int ROWS, int MODE, bool VEC>
-__global__ __launch_bounds__(64) void rms_seq_kernel(NormArgs a) {
+__global__ __launch_bounds__(64) void rms_seq_kernel(ATLAS_NORM_KPARAMS) {
+    ATLAS_NORM_UNPACK;
     extern __shared__ float lds[];
     const uint32_t lane = threadIdx.x;
     const uint32_t h = a.hidden;
@@ -156,7 +177,8 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // Wide engine: one wave per row, 4 rows per 256-thread block.
 template <int MODE, bool VEC>
-__global__ __launch_bounds__(256) void rms_wide_kernel(NormArgs a) {
+__global__ __launch_bounds__(256) void rms_wide_kernel(ATLAS_NORM_KPARAMS) {
+    ATLAS_NORM_UNPACK;
     const uint32_t lane = threadIdx.x & (kWave - 1);
     const uint32_t row = blockIdx.x * 4 + threadIdx.x / kWave;
     if (row >= a.rows) return;
@@ -321,13 +343,13 @@ struct TreeRow {
 };
 
 template <int J, int MODE, bool PAIR, bool DEFER = false, int POL = -1>
-__global__ __launch_bounds__(256) void rms_tree_kernel(NormArgs a) {
+__global__ __launch_bounds__(256) void rms_tree_kernel(ATLAS_NORM_KPARAMS) {
+    ATLAS_NORM_UNPACK;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
-    const uint32_t wpb = blockDim.x >> 6;  // wavefronts per workgroup (1 or 4)
     const uint32_t r0 = blockIdx.x * wpb + wave;
     if (r0 >= a.rows) return;  // wavefront-uniform
-    const uint32_t r1 = r0 + gridDim.x * wpb;
+    const uint32_t r1 = r0 + pair_stride;
     const bool second = PAIR && r1 < a.rows;
     const uint32_t nv = a.hidden >> 2;
     const float* operand = MODE == kNormAddScale ? a.out : a.residual;
@@ -387,7 +409,8 @@ struct FoldScansLds {
 constexpr int kRunHelpers = 4;
 
 template <int R, int J, int MODE, bool PAR, bool STAGE, bool RUN>
-__global__ __launch_bounds__(RUN ? 64 * (kRunHelpers + 1) : 64) void rms_reg_kernel(NormArgs a) {
+__global__ __launch_bounds__(RUN ? 64 * (kRunHelpers + 1) : 64) void rms_reg_kernel(ATLAS_NORM_KPARAMS) {
+    ATLAS_NORM_UNPACK;
     // Squares of R rows, (hidden/4 + 1) float4 per row.  The load phase is
     // straight-line code (rows past the end and columns past the row width
     // are clamped to valid duplicate addresses and never stored), so the
@@ -695,18 +718,18 @@ hipError_t launch_reg_rj(hipStream_t s, const NormArgs& a, bool par) {
     if constexpr (R == 1 && J > 1) {
         if (run) {
             hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, true>), grid, dim3((kRunHelpers + 1) * kWave),
-                               lds, s, a);
+                               lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
             return hipGetLastError();
         }
     }
     if (par && stage)
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, true, false>), grid, dim3(kWave), lds, s, a);
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, true, false>), grid, dim3(kWave), lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
     else if (par)
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, false>), grid, dim3(kWave), lds, s, a);
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, false>), grid, dim3(kWave), lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
     else if (stage)
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, true, false>), grid, dim3(kWave), lds, s, a);
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, true, false>), grid, dim3(kWave), lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
     else
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, false, false>), grid, dim3(kWave), lds, s, a);
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, false, false>), grid, dim3(kWave), lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
     return hipGetLastError();
 }
 
@@ -757,10 +780,14 @@ hipError_t launch_tree_j(hipStream_t s, const NormArgs& a) {
     const uint32_t waves = pair ? (a.rows + 1) / 2 : a.rows;
     const uint32_t wpb = tree_waves_per_group(a.rows);
     const dim3 grid((waves + wpb - 1) / wpb);
+    // a wavefront's second row is G = grid * wpb rows after its first
+    const uint32_t pair_stride = grid.x * wpb;
     if (pair)
-        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, true, kDefer, kStorePolicy>), grid, dim3(64 * wpb), 0, s, a);
+        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, true, kDefer, kStorePolicy>), grid, dim3(64 * wpb), 0, s,
+                           ATLAS_NORM_KARGS(a, wpb, pair_stride));
     else
-        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, false, kDefer, kStorePolicy>), grid, dim3(64 * wpb), 0, s, a);
+        hipLaunchKernelGGL((rms_tree_kernel<J, MODE, false, kDefer, kStorePolicy>), grid, dim3(64 * wpb), 0, s,
+                           ATLAS_NORM_KARGS(a, wpb, pair_stride));
     return hipGetLastError();
 }
 
@@ -797,9 +824,9 @@ hipError_t launch_seq_rows(hipStream_t s, const NormArgs& a, bool vec) {
     const size_t lds = (static_cast<size_t>(ROWS) * stride + ROWS) * sizeof(float);
     const dim3 grid((a.rows + ROWS - 1) / ROWS);
     if (vec)
-        hipLaunchKernelGGL((rms_seq_kernel<ROWS, MODE, true>), grid, dim3(kWave), lds, s, a);
+        hipLaunchKernelGGL((rms_seq_kernel<ROWS, MODE, true>), grid, dim3(kWave), lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
     else
-        hipLaunchKernelGGL((rms_seq_kernel<ROWS, MODE, false>), grid, dim3(kWave), lds, s, a);
+        hipLaunchKernelGGL((rms_seq_kernel<ROWS, MODE, false>), grid, dim3(kWave), lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
     return hipGetLastError();
 }
 
@@ -818,9 +845,9 @@ template <int MODE>
 hipError_t launch_wide(hipStream_t s, const NormArgs& a, bool vec) {
     const dim3 grid((a.rows + 3) / 4);
     if (vec)
-        hipLaunchKernelGGL((rms_wide_kernel<MODE, true>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((rms_wide_kernel<MODE, true>), grid, dim3(256), 0, s, ATLAS_NORM_KARGS(a, 4u, 0u));
     else
-        hipLaunchKernelGGL((rms_wide_kernel<MODE, false>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((rms_wide_kernel<MODE, false>), grid, dim3(256), 0, s, ATLAS_NORM_KARGS(a, 4u, 0u));
     return hipGetLastError();
 }
 
@@ -1098,17 +1125,19 @@ struct TreeRowF16 {
     }
 };
 
+// Parameters in kernarg-preload order (the counts and the pointers the
+// first loads need in the first 56 bytes, as ATLAS_NORM_KPARAMS); wpb and
+// pair_stride as there.
 template <int J, bool ADD, bool PAIR>
-__global__ __launch_bounds__(256) void rms_tree_f16_kernel(const uint16_t* x, const uint16_t* residual,
-                                                           const uint16_t* weight, uint16_t* residual_out,
-                                                           uint16_t* out, uint32_t rows, uint32_t hidden,
-                                                           float epsilon) {
+__global__ __launch_bounds__(256) void rms_tree_f16_kernel(uint32_t rows, uint32_t hidden, uint32_t wpb,
+                                                           uint32_t pair_stride, const uint16_t* x,
+                                                           const uint16_t* residual, const uint16_t* weight,
+                                                           float epsilon, uint16_t* residual_out, uint16_t* out) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
-    const uint32_t wpb = blockDim.x >> 6;  // wavefronts per workgroup (1 or 4)
     const uint32_t r0 = blockIdx.x * wpb + wave;
     if (r0 >= rows) return;  // wavefront-uniform
-    const uint32_t r1 = r0 + gridDim.x * wpb;
+    const uint32_t r1 = r0 + pair_stride;
     const bool second = PAIR && r1 < rows;
     const uint32_t n8 = hidden >> 3;
     TreeRowF16<J, ADD> row0, row1;
@@ -1244,12 +1273,13 @@ hipError_t launch_f16_tree_j(hipStream_t s, const uint16_t* x, const uint16_t* r
     const uint32_t waves = pair ? (rows + 1) / 2 : rows;
     const uint32_t wpb = tree_waves_per_group(rows);
     const dim3 grid((waves + wpb - 1) / wpb);
+    const uint32_t pair_stride = grid.x * wpb;
     if (pair)
-        hipLaunchKernelGGL((rms_tree_f16_kernel<J, ADD, true>), grid, dim3(64 * wpb), 0, s, x, residual, weight,
-                           residual_out, out, rows, hidden, eps);
+        hipLaunchKernelGGL((rms_tree_f16_kernel<J, ADD, true>), grid, dim3(64 * wpb), 0, s, rows, hidden, wpb,
+                           pair_stride, x, residual, weight, eps, residual_out, out);
     else
-        hipLaunchKernelGGL((rms_tree_f16_kernel<J, ADD, false>), grid, dim3(64 * wpb), 0, s, x, residual, weight,
-                           residual_out, out, rows, hidden, eps);
+        hipLaunchKernelGGL((rms_tree_f16_kernel<J, ADD, false>), grid, dim3(64 * wpb), 0, s, rows, hidden, wpb,
+                           pair_stride, x, residual, weight, eps, residual_out, out);
     return hipGetLastError();
 }
 

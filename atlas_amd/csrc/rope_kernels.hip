@@ -254,11 +254,15 @@ __device__ __forceinline__ void sq_p(float* dst, const pvec<P>& x) {
 // MAXU each (TPW = 1).  SEQ = false (ATLAS_REDUCTION_WIDE): each unit's sum
 // of squares is a wavefront tree sum of the lanes' partial sums instead of
 // the in-order fold (no LDS), tolerance-level against the CPU operator.
+// Parameter order: what the first loads' addresses need (the counts, the
+// rows, cos/sin) and epsilon fill the first 56 bytes, which arrive in SGPRs
+// at wave launch (kernarg preload); the weights and outputs, needed only
+// after the fold, follow.
 template <int P, int MAXU, int TPW, int WPG, bool SPLIT = false, bool SEQ = true>
 __global__ __launch_bounds__(64 * WPG) void qk_norm_rope_token_kernel(
-    const float* q, const float* k, const float* q_weight, const float* k_weight, const float* cosine,
-    const float* sine, float* q_out, float* k_out, uint32_t tokens, uint32_t q_heads, uint32_t has_key,
-    uint32_t rope_stride, float epsilon) {
+    uint32_t tokens, uint32_t q_heads, uint32_t has_key, uint32_t rope_stride, const float* q, const float* k,
+    const float* cosine, const float* sine, float epsilon, const float* q_weight, const float* k_weight,
+    float* q_out, float* k_out) {
     constexpr uint32_t HALF = 64 * P;
     constexpr uint32_t D = 2 * HALF;
     constexpr uint32_t STRIDE = D + 4;
@@ -401,8 +405,8 @@ hipError_t launch_qk_token_cfg(hipStream_t s, const float* q, const float* k, co
     const dim3 grid((waves + WPG - 1) / WPG);
 #define ATLAS_QK_CASE(U)                                                                                          \
     if (total <= U) {                                                                                             \
-        hipLaunchKernelGGL((qk_norm_rope_token_kernel<P, U, TPW, WPG, false, SEQ>), grid, dim3(64 * WPG), 0, s, q, \
-                           k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);                \
+        hipLaunchKernelGGL((qk_norm_rope_token_kernel<P, U, TPW, WPG, false, SEQ>), grid, dim3(64 * WPG), 0, s,      \
+                           tokens, q_heads, has_key, rope_stride, q, k, c, sn, eps, qw, kw, qo, ko);            \
         return hipGetLastError();                                                                                 \
     }
     ATLAS_QK_CASE(1)
@@ -425,7 +429,7 @@ hipError_t launch_qk_split(hipStream_t s, const float* q, const float* k, const 
     const uint64_t waves = static_cast<uint64_t>(tokens) * ((total + U - 1) / U);
     if (waves > 0x7fffffffu) return hipErrorInvalidValue;
     hipLaunchKernelGGL((qk_norm_rope_token_kernel<P, U, 1, 1, true, SEQ>), dim3(static_cast<uint32_t>(waves)), dim3(64), 0,
-                       s, q, k, qw, kw, c, sn, qo, ko, tokens, q_heads, has_key, rope_stride, eps);
+                       s, tokens, q_heads, has_key, rope_stride, q, k, c, sn, eps, qw, kw, qo, ko);
     return hipGetLastError();
 }
 
@@ -798,12 +802,15 @@ __device__ __forceinline__ uint32_t rope_partner(uint32_t own, uint32_t G) {
         return static_cast<uint32_t>(__shfl_xor(static_cast<int>(own), static_cast<int>(G), kWave));
 }
 
+// Parameter order: the counts, the input rows and cos/sin fill the first 56
+// bytes, which arrive in SGPRs at wave launch (kernarg preload); the
+// outputs, needed only at the stores, follow.
 template <bool F16, int NI, int GSH>
-__global__ __launch_bounds__(256) void rope_half_token_kernel(const uint8_t* x0, uint8_t* out0, uint32_t heads0,
-                                                              const uint8_t* x1, uint8_t* out1, uint32_t heads1,
-                                                              const float* cosine, const float* sine,
-                                                              uint32_t tokens, uint32_t head_dim,
-                                                              uint32_t rope_stride, uint32_t g_shift_rt) {
+__global__ __launch_bounds__(256) void rope_half_token_kernel(uint32_t tokens, uint32_t head_dim, uint32_t heads0,
+                                                              uint32_t heads1, uint32_t rope_stride,
+                                                              uint32_t g_shift_rt, const uint8_t* x0,
+                                                              const uint8_t* x1, const float* cosine,
+                                                              const float* sine, uint8_t* out0, uint8_t* out1) {
     constexpr uint32_t V = F16 ? 8 : 4;
     constexpr uint32_t kEsz = F16 ? 2 : 4;
     constexpr bool kMirror = GSH >= 0;
@@ -903,14 +910,14 @@ bool launch_rope_half_token(hipStream_t stream, const void* x0, void* out0, uint
 #define ATLAS_ROPE_TOKEN_CASE(N)                                                                                 \
     case N:                                                                                                      \
         if (g_shift == 2)                                                                                        \
-            hipLaunchKernelGGL((rope_half_token_kernel<F16, N, 2>), grid, dim3(256), 0, stream, a0, b0, heads0, a1, \
-                               b1, heads1, cosine, sine, tokens, head_dim, rope_stride, g_shift);                \
+            hipLaunchKernelGGL((rope_half_token_kernel<F16, N, 2>), grid, dim3(256), 0, stream, tokens, head_dim,   \
+                               heads0, heads1, rope_stride, g_shift, a0, a1, cosine, sine, b0, b1);              \
         else if (g_shift == 3)                                                                                   \
-            hipLaunchKernelGGL((rope_half_token_kernel<F16, N, 3>), grid, dim3(256), 0, stream, a0, b0, heads0, a1, \
-                               b1, heads1, cosine, sine, tokens, head_dim, rope_stride, g_shift);                \
+            hipLaunchKernelGGL((rope_half_token_kernel<F16, N, 3>), grid, dim3(256), 0, stream, tokens, head_dim,   \
+                               heads0, heads1, rope_stride, g_shift, a0, a1, cosine, sine, b0, b1);              \
         else                                                                                                     \
-            hipLaunchKernelGGL((rope_half_token_kernel<F16, N, -1>), grid, dim3(256), 0, stream, a0, b0, heads0,  \
-                               a1, b1, heads1, cosine, sine, tokens, head_dim, rope_stride, g_shift);            \
+            hipLaunchKernelGGL((rope_half_token_kernel<F16, N, -1>), grid, dim3(256), 0, stream, tokens, head_dim, \
+                               heads0, heads1, rope_stride, g_shift, a0, a1, cosine, sine, b0, b1);              \
         return true;
     switch (ni) {
         ATLAS_ROPE_TOKEN_CASE(1) ATLAS_ROPE_TOKEN_CASE(2) ATLAS_ROPE_TOKEN_CASE(3) ATLAS_ROPE_TOKEN_CASE(4)
