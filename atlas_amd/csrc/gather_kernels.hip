@@ -293,7 +293,7 @@ __global__ __launch_bounds__(256) void ple_seg_kernel(const uint8_t* __restrict_
     const uint32_t seg_bytes = Q6 ? (seg_vals / 256) * 210 : (seg_vals / 32) * 18;
     if (valid)
         stage_row<1, 4, 8>(seg, table + static_cast<size_t>(id) * row_bytes + seg_off, seg_bytes, threadIdx.x,
-                           blockDim.x);
+                           256u);  // the launch's workgroup size (no implicit-argument load)
     __syncthreads();
     const auto ro = span_rsrc(out + base, row_elems * 4u);
 #pragma unroll

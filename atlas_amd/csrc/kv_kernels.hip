@@ -105,9 +105,22 @@ __device__ __forceinline__ void encode_block(float v, uint8_t* dst, uint32_t j) 
     }
 }
 
+// Kernel parameters of the KV-append kernels: KvAppendArgs field by field
+// (a by-value struct is not preloaded into SGPRs), the counts and positions
+// first; all 48 bytes arrive in user SGPRs at wave launch (kernarg preload),
+// so the position and row loads wait on no scalar load.
+#define ATLAS_KV_KPARAMS                                                                                  \
+    uint32_t p_kv_width, uint32_t p_capacity, uint32_t p_tokens, float p_epsilon, const uint32_t* p_positions, \
+        const float* p_key, const float* p_value, uint8_t* p_cache
+#define ATLAS_KV_UNPACK \
+    const KvAppendArgs a { p_key, p_value, p_cache, p_positions, p_kv_width, p_capacity, p_tokens, p_epsilon }
+#define ATLAS_KV_KARGS(a) \
+    (a).kv_width, (a).capacity, (a).tokens, (a).epsilon, (a).positions, (a).key, (a).value, (a).cache
+
 // P: values per thread and row (kv_width <= 256 * P).
 template <int FMT, bool VNORM, int P>
-__global__ __launch_bounds__(256) void kv_append_kernel(KvAppendArgs a) {
+__global__ __launch_bounds__(256) void kv_append_kernel(ATLAS_KV_KPARAMS) {
+    ATLAS_KV_UNPACK;
     extern __shared__ __align__(16) float sq[];  // kv_width squares of V (VNORM)
     __shared__ float inv_shared;
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
@@ -487,7 +500,8 @@ __device__ __forceinline__ void keep_alive(const PendingStore& st) {
 }
 
 template <int FMT, bool VNORM, int V4>
-__global__ __launch_bounds__(256) void kv_append_row_kernel(KvAppendArgs a) {
+__global__ __launch_bounds__(256) void kv_append_row_kernel(ATLAS_KV_KPARAMS) {
+    ATLAS_KV_UNPACK;
     constexpr uint32_t kW = 256u * V4;
     constexpr uint32_t kRowBytes = FMT == kKvF32 ? kW * 4 : (kW / 32) * (FMT == kKvQ8_0 ? 34u : 18u);
     __shared__ __align__(16) f32x4 sq[2][VNORM ? 64 * V4 : 1];
@@ -544,7 +558,8 @@ struct RowsShape {
 };
 
 template <int FMT, int TW, int NW>
-__global__ __launch_bounds__((NW + 1) * 64) void kv_append_rows_kernel(KvAppendArgs a) {
+__global__ __launch_bounds__((NW + 1) * 64) void kv_append_rows_kernel(ATLAS_KV_KPARAMS) {
+    ATLAS_KV_UNPACK;
     constexpr uint32_t kW = 256;
     constexpr uint32_t kTok = RowsShape<TW, NW>::kTokens;
     constexpr uint32_t kRowBytes = FMT == kKvF32 ? kW * 4 : (kW / 32) * (FMT == kKvQ8_0 ? 34u : 18u);
@@ -653,15 +668,15 @@ bool launch_row(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
         constexpr int kTw = FMT == kKvF32 ? 2 : 1;
         using Shape = RowsShape<kTw, 4>;
         hipLaunchKernelGGL((kv_append_rows_kernel<FMT, kTw, 4>), dim3((a.tokens + Shape::kTokens - 1) / Shape::kTokens),
-                           dim3(Shape::kThreads), 0, stream, a);
+                           dim3(Shape::kThreads), 0, stream, ATLAS_KV_KARGS(a));
         return true;
     }
     const dim3 grid((a.tokens + 1) / 2);
 #define ATLAS_KV_ROW(V)                                                                          \
     if (vnorm)                                                                                   \
-        hipLaunchKernelGGL((kv_append_row_kernel<FMT, true, V>), grid, dim3(256), 0, stream, a);  \
+        hipLaunchKernelGGL((kv_append_row_kernel<FMT, true, V>), grid, dim3(256), 0, stream, ATLAS_KV_KARGS(a)); \
     else                                                                                         \
-        hipLaunchKernelGGL((kv_append_row_kernel<FMT, false, V>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((kv_append_row_kernel<FMT, false, V>), grid, dim3(256), 0, stream, ATLAS_KV_KARGS(a));
     if (w == 256) {
         ATLAS_KV_ROW(1)
     } else if (w == 512) {
@@ -677,9 +692,9 @@ template <int FMT, int P>
 hipError_t launch_p(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
     if (vnorm)
         hipLaunchKernelGGL((kv_append_kernel<FMT, true, P>), dim3(a.tokens), dim3(kThreads),
-                           a.kv_width * sizeof(float), stream, a);
+                           a.kv_width * sizeof(float), stream, ATLAS_KV_KARGS(a));
     else
-        hipLaunchKernelGGL((kv_append_kernel<FMT, false, P>), dim3(a.tokens), dim3(kThreads), 0, stream, a);
+        hipLaunchKernelGGL((kv_append_kernel<FMT, false, P>), dim3(a.tokens), dim3(kThreads), 0, stream, ATLAS_KV_KARGS(a));
     return hipGetLastError();
 }
 

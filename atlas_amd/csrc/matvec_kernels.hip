@@ -323,8 +323,20 @@ hipError_t launch_lpr(hipStream_t stream, MatvecArgs a) {
 // ---------------------------------------------------------------------------
 constexpr uint32_t kPleMaxGroups = 1024;
 
+// Kernel parameters of the PLE projection: PleProjArgs field by field (a
+// by-value struct is not preloaded into SGPRs), counts first; all 56 bytes
+// arrive in user SGPRs at wave launch (kernarg preload).
+#define ATLAS_PP_KPARAMS                                                                                 \
+    uint32_t p_hidden, uint32_t p_width, uint32_t p_groups, float p_scale, float p_epsilon,                \
+        const float* p_input, const uint16_t* p_weights, const float* p_norm_weight, float* p_output
+#define ATLAS_PP_UNPACK \
+    const PleProjArgs a { p_input, p_weights, p_norm_weight, p_output, p_hidden, p_width, p_groups, p_scale, p_epsilon }
+#define ATLAS_PP_KARGS(a) \
+    (a).hidden, (a).width, (a).groups, (a).scale, (a).epsilon, (a).input, (a).weights, (a).norm_weight, (a).output
+
 template <int HC, int RPW>
-__global__ __launch_bounds__(256) void ple_proj_f16_kernel(PleProjArgs a) {
+__global__ __launch_bounds__(256) void ple_proj_f16_kernel(ATLAS_PP_KPARAMS) {
+    ATLAS_PP_UNPACK;
     const uint32_t tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     const uint32_t hidden = a.hidden;
     const uint32_t row0 = blockIdx.x * (4 * RPW) + wave * RPW;
@@ -407,7 +419,8 @@ hipError_t launch_ple_projection_f16(hipStream_t stream, const PleProjArgs& a) {
     constexpr int kRpw = 2;
     const dim3 grid(a.groups * a.width / (4 * kRpw));
     const uint32_t hc = (a.hidden + 511) / 512;
-#define ATLAS_PLE_PROJ(H) hipLaunchKernelGGL((ple_proj_f16_kernel<H, kRpw>), grid, dim3(kWaves * kWave), 0, stream, a)
+#define ATLAS_PLE_PROJ(H) hipLaunchKernelGGL((ple_proj_f16_kernel<H, kRpw>), grid, dim3(kWaves * kWave), 0, stream, \
+                                            ATLAS_PP_KARGS(a))
     if (hc <= 1)
         ATLAS_PLE_PROJ(1);
     else if (hc <= 2)

@@ -729,14 +729,16 @@ hipError_t launch_qk_norm_rope_f32(hipStream_t stream, Reduction red, const floa
 
 // Two tensors sharing the cos/sin rows (Q and K of the same tokens): threads
 // [0, tokens*heads0*groups) rotate x0, the following ones x1; heads1 = 0
-// rotates one tensor.
+// rotates one tensor.  Parameters in kernarg-preload order: the counts, the inputs and
+// cos/sin fill the first 56 bytes (user SGPRs at wave launch), the outputs
+// follow.
 template <int P>
-__global__ __launch_bounds__(256) void rope_half_f32_kernel(const float* x0, float* out0, uint32_t heads0,
-                                                            const float* x1, float* out1, uint32_t heads1,
-                                                            const float* cosine, const float* sine, uint32_t tokens,
-                                                            uint32_t head_dim, uint32_t rope_stride) {
+__global__ __launch_bounds__(256) void rope_half_f32_kernel(uint32_t tokens, uint32_t head_dim,
+                                                            uint32_t rope_stride, uint32_t heads0, uint32_t heads1,
+                                                            const float* x0, const float* x1, const float* cosine,
+                                                            const float* sine, float* out0, float* out1) {
     const uint32_t groups = (head_dim / 2) / P;
-    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;  // 256-thread workgroups
     const uint64_t total0 = static_cast<uint64_t>(tokens) * heads0 * groups;
     const uint64_t total1 = static_cast<uint64_t>(tokens) * heads1 * groups;
     const bool second = i >= total0;
@@ -752,12 +754,12 @@ __global__ __launch_bounds__(256) void rope_half_f32_kernel(const float* x0, flo
 }
 
 template <int P>
-__global__ __launch_bounds__(256) void rope_half_f16_kernel(const uint16_t* x0, uint16_t* out0, uint32_t heads0,
-                                                            const uint16_t* x1, uint16_t* out1, uint32_t heads1,
-                                                            const float* cosine, const float* sine, uint32_t tokens,
-                                                            uint32_t head_dim, uint32_t rope_stride) {
+__global__ __launch_bounds__(256) void rope_half_f16_kernel(uint32_t tokens, uint32_t head_dim,
+                                                            uint32_t rope_stride, uint32_t heads0, uint32_t heads1,
+                                                            const uint16_t* x0, const uint16_t* x1, const float* cosine,
+                                                            const float* sine, uint16_t* out0, uint16_t* out1) {
     const uint32_t groups = (head_dim / 2) / P;
-    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x;  // 256-thread workgroups
     const uint64_t total0 = static_cast<uint64_t>(tokens) * heads0 * groups;
     const uint64_t total1 = static_cast<uint64_t>(tokens) * heads1 * groups;
     const bool second = i >= total0;
@@ -941,11 +943,11 @@ hipError_t launch_rope_half_pair_f32(hipStream_t stream, const float* x0, float*
     const uint64_t threads = static_cast<uint64_t>(tokens) * (static_cast<uint64_t>(heads0) + heads1) * (half / P);
     const dim3 grid(static_cast<uint32_t>((threads + 255) / 256));
     if (vec)
-        hipLaunchKernelGGL((rope_half_f32_kernel<4>), grid, dim3(256), 0, stream, x0, out0, heads0, x1, out1, heads1,
-                           cosine, sine, tokens, head_dim, rope_stride);
+        hipLaunchKernelGGL((rope_half_f32_kernel<4>), grid, dim3(256), 0, stream, tokens, head_dim, rope_stride,
+                           heads0, heads1, x0, x1, cosine, sine, out0, out1);
     else
-        hipLaunchKernelGGL((rope_half_f32_kernel<1>), grid, dim3(256), 0, stream, x0, out0, heads0, x1, out1, heads1,
-                           cosine, sine, tokens, head_dim, rope_stride);
+        hipLaunchKernelGGL((rope_half_f32_kernel<1>), grid, dim3(256), 0, stream, tokens, head_dim, rope_stride,
+                           heads0, heads1, x0, x1, cosine, sine, out0, out1);
     return hipGetLastError();
 }
 
@@ -963,11 +965,11 @@ hipError_t launch_rope_half_pair_f16(hipStream_t stream, const uint16_t* x0, uin
     const uint64_t threads = static_cast<uint64_t>(tokens) * (static_cast<uint64_t>(heads0) + heads1) * (half / P);
     const dim3 grid(static_cast<uint32_t>((threads + 255) / 256));
     if (vec)
-        hipLaunchKernelGGL((rope_half_f16_kernel<8>), grid, dim3(256), 0, stream, x0, out0, heads0, x1, out1, heads1,
-                           cosine, sine, tokens, head_dim, rope_stride);
+        hipLaunchKernelGGL((rope_half_f16_kernel<8>), grid, dim3(256), 0, stream, tokens, head_dim, rope_stride,
+                           heads0, heads1, x0, x1, cosine, sine, out0, out1);
     else
-        hipLaunchKernelGGL((rope_half_f16_kernel<1>), grid, dim3(256), 0, stream, x0, out0, heads0, x1, out1, heads1,
-                           cosine, sine, tokens, head_dim, rope_stride);
+        hipLaunchKernelGGL((rope_half_f16_kernel<1>), grid, dim3(256), 0, stream, tokens, head_dim, rope_stride,
+                           heads0, heads1, x0, x1, cosine, sine, out0, out1);
     return hipGetLastError();
 }
 
