@@ -68,3 +68,26 @@ def q4_0_dequant_numpy(weights: np.ndarray, rows: int, input_width: int) -> np.n
     q = b[:, :, 2:].astype(np.int64)
     vals = np.concatenate([(q & 15) - 8, (q >> 4) - 8], axis=2).astype(np.float64)
     return (vals * d[:, :, None]).reshape(rows, input_width)
+
+
+def kv_tie_blocks():
+    """Two blocks whose encodings depend on the tie rules, with their bytes
+    derived by hand from the reference's steps (kernels.metal:1222-1256):
+    - Q8_0: max |v| = 127, so the scale is exactly 1 and every quotient v/s
+      is v; Metal's round() takes halfway cases away from zero, so 2.5 -> 3,
+      -2.5 -> -3, 0.5 -> 1, -0.5 -> -1, 126.5 -> 127 (half-even: 2, -2, 0, 0,
+      126).
+    - Q4_0: |v| = 4 at index 0 (-4) and index 1 (+4); the forward scan's
+      strict > keeps the first, so the signed maximum is -4 and the scale
+      -4 / -8 = 0.5 (f16 0x3800); codes int(v / 0.5 + 8.5) clamped to
+      [0, 15]: -4 -> 0, 4 -> 15, and v_j = (j - 16) / 4 for j >= 2 ->
+      int(j / 2 + 1 / 2) = (j + 1) // 2, clamped (the last maximum would give
+      scale -0.5, 0xB800, and mirrored codes)."""
+    q8 = np.zeros(32, np.float32)
+    q8[:10] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.5, -1.5, 126.5, -126.5, 3.0]
+    codes8 = [127, 3, -3, 1, -1, 2, -2, 127, -127, 3] + [0] * 22
+    want8 = bytes([0x00, 0x3C]) + bytes((c & 0xFF) for c in codes8)
+    q4 = np.array([-4.0, 4.0] + [(j - 16) / 4.0 for j in range(2, 32)], np.float32)
+    codes4 = [0, 15] + [min((j + 1) // 2, 15) for j in range(2, 32)]
+    want4 = bytes([0x00, 0x38]) + bytes(codes4[i] | (codes4[i + 16] << 4) for i in range(16))
+    return q8, want8, q4, want4

@@ -127,3 +127,23 @@ def test_kv_append_invalid_input(rt):
         with pytest.raises(OperatorError) as e:
             bad()
         assert e.value.kind == "InvalidInput"
+
+
+@pytest.mark.parametrize("fmt", ["q8_0", "q4_0"])
+def test_kv_append_tie_rules_known_answers(rt, ora, fmt):
+    """The hand-derived blocks of matvec_cases.kv_tie_blocks (quotients on
+    half-integers for Q8_0's half-away rounding, +-4 as the largest |v| for
+    Q4_0's first-maximum rule) tiled over a K and a V row: every block of the
+    device cache equals the hand-derived bytes, on the row engine (width 256)
+    and the per-value engine (width 64)."""
+    q8, want8, q4, want4 = mc.kv_tie_blocks()
+    blk, want = (q8, want8) if fmt == "q8_0" else (q4, want4)
+    for w in (256, 64):
+        row = np.tile(blk, w // 32).astype(f32)
+        say(f"kv {fmt} tie-rule blocks w={w}")
+        got, exp, _ = run(rt, ora, fmt, row, row.copy(), w, 2, [1], False)
+        assert_cache(f"{fmt} tie blocks w={w}", got, exp)
+        rb = ora.kv_row_bytes(fmt, w)
+        for side in (0, 1):  # K and V rows of position 1
+            r = got[(side * 2 + 1) * rb:(side * 2 + 2) * rb]
+            assert r.tobytes() == want * (w // 32), (fmt, w, side)

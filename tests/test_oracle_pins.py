@@ -13,6 +13,8 @@ import os
 import numpy as np
 import pytest
 
+import matvec_cases as mc
+
 HERE = os.path.dirname(os.path.abspath(__file__))
 KATS = json.load(open(os.path.join(HERE, "golden", "kats.json")))
 f32 = np.float32
@@ -735,6 +737,24 @@ def test_kv_encoders_pinned(ora):
     d8 = np.frombuffer(b8[:2].tobytes(), np.float16).astype(np.float64)[0]
     dq8 = b8[2:].view(np.int8).astype(np.float64) * d8
     assert np.all(np.abs(dq8 - kat) <= 0.03)
+
+
+def test_kv_encoder_tie_rules_known_answers(ora):
+    """The oracle's encoders give the hand-derived bytes of kv_tie_blocks, and
+    the same check rejects encoders with the other tie rules (planted
+    mistakes: round-half-even quotients, the last largest |v|)."""
+    q8, want8, q4, want4 = mc.kv_tie_blocks()
+    assert bytes(ora.encode_q8_0_block(q8)) == want8
+    assert bytes(ora.encode_q4_0_block(q4)) == want4
+    # planted: round half to even (numpy's rint) instead of half away from zero
+    even = np.rint(q8 / f32(1.0)).astype(np.int8)
+    assert bytes([0x00, 0x3C]) + even.view(np.uint8).tobytes() != want8
+    # planted: the last index of the largest |v| gives the signed maximum
+    last = 31 - int(np.argmax(np.abs(q4)[::-1]))
+    scale = f32(q4[last] / f32(-8))
+    codes = np.clip(np.trunc(q4 / scale + f32(8.5)), 0, 15).astype(np.uint8)
+    planted = np.array([scale], np.float16).view(np.uint8).tobytes() + bytes(int(codes[i]) | (int(codes[i + 16]) << 4) for i in range(16))
+    assert planted != want4
 
 
 def test_kv_encoder_error_bounds(ora):
