@@ -694,7 +694,8 @@ hipError_t launch_p(hipStream_t stream, const KvAppendArgs& a, bool vnorm) {
         hipLaunchKernelGGL((kv_append_kernel<FMT, true, P>), dim3(a.tokens), dim3(kThreads),
                            a.kv_width * sizeof(float), stream, ATLAS_KV_KARGS(a));
     else
-        hipLaunchKernelGGL((kv_append_kernel<FMT, false, P>), dim3(a.tokens), dim3(kThreads), 0, stream, ATLAS_KV_KARGS(a));
+        hipLaunchKernelGGL((kv_append_kernel<FMT, false, P>), dim3(a.tokens), dim3(kThreads), 0, stream,
+                           ATLAS_KV_KARGS(a));
     return hipGetLastError();
 }
 

@@ -723,13 +723,17 @@ hipError_t launch_reg_rj(hipStream_t s, const NormArgs& a, bool par) {
         }
     }
     if (par && stage)
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, true, false>), grid, dim3(kWave), lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, true, false>), grid, dim3(kWave), lds, s,
+                           ATLAS_NORM_KARGS(a, 1u, 0u));
     else if (par)
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, false>), grid, dim3(kWave), lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, true, false, false>), grid, dim3(kWave), lds, s,
+                           ATLAS_NORM_KARGS(a, 1u, 0u));
     else if (stage)
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, true, false>), grid, dim3(kWave), lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, true, false>), grid, dim3(kWave), lds, s,
+                           ATLAS_NORM_KARGS(a, 1u, 0u));
     else
-        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, false, false>), grid, dim3(kWave), lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
+        hipLaunchKernelGGL((rms_reg_kernel<R, J, MODE, false, false, false>), grid, dim3(kWave), lds, s,
+                           ATLAS_NORM_KARGS(a, 1u, 0u));
     return hipGetLastError();
 }
 
@@ -824,9 +828,11 @@ hipError_t launch_seq_rows(hipStream_t s, const NormArgs& a, bool vec) {
     const size_t lds = (static_cast<size_t>(ROWS) * stride + ROWS) * sizeof(float);
     const dim3 grid((a.rows + ROWS - 1) / ROWS);
     if (vec)
-        hipLaunchKernelGGL((rms_seq_kernel<ROWS, MODE, true>), grid, dim3(kWave), lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
+        hipLaunchKernelGGL((rms_seq_kernel<ROWS, MODE, true>), grid, dim3(kWave), lds, s,
+                           ATLAS_NORM_KARGS(a, 1u, 0u));
     else
-        hipLaunchKernelGGL((rms_seq_kernel<ROWS, MODE, false>), grid, dim3(kWave), lds, s, ATLAS_NORM_KARGS(a, 1u, 0u));
+        hipLaunchKernelGGL((rms_seq_kernel<ROWS, MODE, false>), grid, dim3(kWave), lds, s,
+                           ATLAS_NORM_KARGS(a, 1u, 0u));
     return hipGetLastError();
 }
 
