@@ -86,11 +86,22 @@ __device__ __forceinline__ void q6_k_decode4(const uint8_t* row, uint32_t col, f
     // the four 6-bit codes as the bytes of one word: low nibbles and high
     // bit pairs extracted four at a time (q_j = byte j, 0..63)
     const uint32_t codes = ((ql >> lshift) & 0x0f0f0f0fu) | (((qh >> (2 * st)) & 0x03030303u) << 4);
+    // The reference's (q * sc) * d as q * (sc * d): q * sc is exact (|q| <= 32,
+    // |sc| <= 128) and so is sc * d (a 7-bit integer times an 11-bit f16
+    // significand), so both are the one rounding of q * sc * d; a zero's sign
+    // is the XOR of the three factors' signs in either grouping, and a NaN or
+    // infinite d propagates alike.  One product per pass instead of one per
+    // value.
+    const float sd = sc * d;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        // float(q - 32) == float(q) - 32 exactly (small integers)
-        const float q = static_cast<float>((codes >> (8 * j)) & 0xffu) - 32.0f;
-        v[j] = q * sc * d;
+        // byte j to float in one conversion (v_cvt_f32_ubyte<j>); the empty
+        // asm keeps the compiler from turning float(q) - 32 back into an
+        // integer subtraction and a conversion.  float(q) - 32 ==
+        // float(q - 32) exactly (small integers; q = 32 gives +0 either way).
+        float q = static_cast<float>((codes >> (8 * j)) & 0xffu);
+        __asm__("" : "+v"(q));
+        v[j] = (q - 32.0f) * sd;
     }
 }
 
