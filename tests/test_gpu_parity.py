@@ -327,6 +327,41 @@ def test_embed_quant_shapes(rt, ora, fmt, hidden, tokens):
     assert_bits(f"embed {fmt}", cases.embed_q_gpu(rt, inp, m), cases.embed_q_oracle(ora, inp, m))
 
 
+# f16 scale patterns: +-0, subnormals, +-max, +-inf and NaNs with payloads
+_SPECIAL_D = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x8001, 0x7BFF, 0xFBFF, 0x7C00, 0xFC00, 0x7E00, 0xFE00,
+                       0x7C01, 0x3C00, 0xBC00], np.uint16)
+
+
+@pytest.mark.parametrize("fmt", ["q6_k", "q4_0"])
+def test_embed_quant_special_scales(rt, ora, fmt):
+    """Block scales d cycling through +-0, subnormals, +-max, +-inf and NaNs,
+    with zero codes (q = 32 for Q6_K, nibble 8 for Q4_0) and Q6_K sub-scales
+    of 0, -128 and 127 in every block: the device gather equals the oracle
+    bit for bit, NaNs equal to NaNs (the Q6_K decode forms sc * d once per
+    super-block, the reference (q * sc) * d)."""
+    vocab, hidden, tokens = 64, 1536, 96
+    inp, m = cases.embed_q_case(vocab, hidden, tokens, 727, fmt == "q6_k", fmt)
+    step = 210 if fmt == "q6_k" else 18
+    t = inp["table"].reshape(-1, step)
+    nblk = t.shape[0]
+    d = _SPECIAL_D[np.arange(nblk) % _SPECIAL_D.size]
+    if fmt == "q6_k":
+        t[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
+        t[:, 192] = 0                               # sub-scale 0
+        t[:, 193] = 0x80                            # -128
+        t[:, 194] = 0x7F                            # 127
+        t[:, 0] = 0x00                              # ql low nibble 0 ...
+        t[:, 128] = 0x02                            # ... with qh bits 2 -> q = 32 (a zero code)
+    else:
+        t[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+        t[:, 2] = 0x88                              # nibbles 8: zero codes
+    inp["table"] = t.reshape(-1)
+    say(f"embed {fmt} special scales")
+    with np.errstate(all="ignore"):
+        exp = cases.embed_q_oracle(ora, inp, m)
+    cases.assert_bits_nan_equal(f"embed {fmt} special scales", cases.embed_q_gpu(rt, inp, m), exp)
+
+
 @pytest.mark.parametrize("fmt", ["q4_0", "q6_k", "q8_0"])
 def test_embed_quant_table_at_any_offset(rt, ora, fmt):
     """The gather stages a row through the 16-byte-aligned span around it:
